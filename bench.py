@@ -1,0 +1,323 @@
+"""Benchmark of the GEMM-shaped hot path on one MI355X.
+
+Default workload (the configuration the headline metric is quoted on):
+aten.convolution as implicit-im2col GEMM, float32 NCHW, batch 1 --
+  2a: x[1,64,80,80]  * w[128,64,3,3]  s1 p1 -> y[1,128,80,80]
+  2b: x[1,128,80,80] * w[256,128,3,3] s2 p1 -> y[1,256,40,40]
+One step = both convolutions, recorded once and replayed with one submit per
+step (one captured HIP graph).  Inputs are resident in HBM before timing.
+
+Printed: ONE JSON line on stdout (the contract).  Per-configuration numbers
+for every other configuration (mm 512^3 fp32, the conv pair in fp16 on MFMA,
+depthwise fp16, addmm fp16 NN/NT, bmm fp16) go to stderr and, with --detail
+PATH, to a JSON file.  Each is measured at shape (single launch per sample)
+and amortised (a graph of many instances rotating over >= 300 MB of distinct
+buffers, so the 256 MB MALL cannot hold the working set); roofline fractions
+quote the amortised number.
+
+The CPU baseline is the oracle's order-faithful C restatement of the
+reference WGSL kernels (Dawn + SwiftShader cannot run offline), timed on this
+host's cores on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK = {  # MI355X published dense peaks
+    "hbm_GBps": 8000.0,
+    "fp16_TFLOPs": 2500.0,
+    "bf16_TFLOPs": 2500.0,
+    "fp32_TFLOPs": 157.3,
+}
+CONV2 = {
+    "2a": dict(x=(1, 64, 80, 80), w=(128, 64, 3, 3), s=(2 - 1, 1), p=(1, 1), y=(1, 128, 80, 80)),
+    "2b": dict(x=(1, 128, 80, 80), w=(256, 128, 3, 3), s=(2, 2), p=(1, 1), y=(1, 256, 40, 40)),
+}
+
+
+def conv_flops(c):
+    _, oc, oh, ow = c["y"]
+    _, icg, kh, kw = c["w"]
+    return 2.0 * oc * oh * ow * icg * kh * kw * c["y"][0]
+
+
+def conv_bytes(c, es):
+    n = int(np.prod(c["x"])) + int(np.prod(c["w"])) + c["w"][0] + int(np.prod(c["y"]))
+    return n * es
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- builders
+def build_conv(ctx, I, c, dtype, seed, bias=True, batch=1):
+    xs = (batch,) + tuple(c["x"][1:])
+    ys = [batch] + list(c["y"][1:])
+    x = I.uniform(seed, xs, -1, 1)
+    w = I.kaiming_uniform(seed + 1, c["w"])
+    tx, tw = ctx.from_numpy(x, dtype), ctx.from_numpy(w, dtype)
+    tb = ctx.from_numpy(I.uniform(seed + 2, (c["w"][0],), -0.1, 0.1), dtype) if bias else None
+    ty = ctx.tensor(dtype, ys)
+    groups = c.get("groups", 1)
+    ctx.convolution(tx, tw, tb, list(c["s"]), list(c["p"]), [1, 1], False, [0, 0], groups, ty)
+    return ctx.last_kernel
+
+
+def time_ctx(ctx, reps, warm=3):
+    for _ in range(warm):
+        ctx.submit()
+    ctx.sync()
+    return ctx.time_submits(reps)
+
+
+def measure(W, build, n_inst_amortised, reps_shape=50, reps_amort=5):
+    """At-shape: one instance, one launch per submit.  Amortised: a graph of
+    n instances with distinct buffers, per-instance time."""
+    ctx = W.Context(0)
+    try:
+        kernel = build(ctx, 0)
+        shape_ms = time_ctx(ctx, reps_shape)
+    finally:
+        ctx.destroy()
+    ctx = W.Context(0)
+    try:
+        for i in range(n_inst_amortised):
+            build(ctx, i)
+        amort_ms = time_ctx(ctx, reps_amort, warm=1) / n_inst_amortised
+    finally:
+        ctx.destroy()
+    return kernel, shape_ms, amort_ms
+
+
+# ---------------------------------------------------------------- detail configs
+def detail_configs(W, I, quick=False):
+    out = {}
+    scale = 0.25 if quick else 1.0
+
+    def rec(name, kernel, shape_ms, amort_ms, flops, nbytes, bound, peak):
+        d = {"kernel": kernel, "at_shape_ms": shape_ms, "amortised_ms": amort_ms,
+             "GFLOPs_at_shape": flops / shape_ms / 1e6, "GFLOPs_amortised": flops / amort_ms / 1e6,
+             "GBps_at_shape": nbytes / shape_ms / 1e6, "GBps_amortised": nbytes / amort_ms / 1e6,
+             "bound": bound}
+        if bound == "hbm":
+            d["frac_of_peak_amortised"] = d["GBps_amortised"] / PEAK["hbm_GBps"]
+        else:
+            d["frac_of_peak_amortised"] = d["GFLOPs_amortised"] / 1e3 / peak
+        out[name] = d
+        log(f"{name:28s} {kernel:34s} shape {shape_ms*1e3:9.2f} us  amort {amort_ms*1e3:9.2f} us  "
+            f"{d['GFLOPs_amortised']:10.1f} GFLOP/s {d['GBps_amortised']:9.1f} GB/s  "
+            f"{100*d['frac_of_peak_amortised']:5.1f}% of {bound}")
+
+    # config 1: mm fp32 512^3
+    def b_mm(ctx, i):
+        a = ctx.from_numpy(I.uniform(2 * i, (512, 512), -1, 1), "float32")
+        b = ctx.from_numpy(I.uniform(2 * i + 1, (512, 512), -1, 1), "float32")
+        o = ctx.tensor("float32", [512, 512])
+        ctx.mm(a, b, o)
+        return ctx.last_kernel
+    k, s, a = measure(W, b_mm, max(8, int(100 * scale)))
+    rec("1_mm_f32_512", k, s, a, 2 * 512 ** 3, 3 * 512 * 512 * 4, "mfma", PEAK["fp32_TFLOPs"])
+
+    # config 2 in both dtypes
+    for dt, es, peak in (("float32", 4, PEAK["fp32_TFLOPs"]), ("float16", 2, PEAK["fp16_TFLOPs"])):
+        for v, c in CONV2.items():
+            n = max(8, int(int(300e6 / conv_bytes(c, es)) * scale))
+            k, s, a = measure(W, lambda ctx, i, c=c, dt=dt: build_conv(ctx, I, c, dt, 10 * i), n)
+            rec(f"2{v[1]}_conv_{dt}", k, s, a, conv_flops(c), conv_bytes(c, es), "mfma", peak)
+            # one launch carrying 64 batch-1 instances (batched-instance form)
+            ctx = W.Context(0)
+            try:
+                kb = build_conv(ctx, I, c, dt, 7, batch=64)
+                ms = time_ctx(ctx, 10)
+            finally:
+                ctx.destroy()
+            out[f"2{v[1]}_conv_{dt}"]["batched64_ms_per_instance"] = ms / 64
+            out[f"2{v[1]}_conv_{dt}"]["GFLOPs_batched64"] = conv_flops(c) * 64 / ms / 1e6
+            out[f"2{v[1]}_conv_{dt}"]["frac_of_peak_batched64"] = conv_flops(c) * 64 / ms / 1e9 / peak
+            log(f"{'':28s} batched x64: {ms/64*1e3:9.2f} us/instance  "
+                f"{conv_flops(c)*64/ms/1e6:10.1f} GFLOP/s  {100*conv_flops(c)*64/ms/1e9/peak:5.1f}%")
+
+    # config 3: depthwise fp16
+    DW = {"3A": dict(x=(1, 256, 40, 40), w=(256, 1, 3, 3), s=(1, 1), p=(1, 1), y=(1, 256, 40, 40), groups=256),
+          "3B": dict(x=(1, 512, 20, 20), w=(512, 1, 5, 5), s=(2, 2), p=(2, 2), y=(1, 512, 10, 10), groups=512)}
+    for v, c in DW.items():
+        nbytes = (int(np.prod(c["x"])) + int(np.prod(c["w"])) + int(np.prod(c["y"]))) * 2
+        n = max(8, int(int(300e6 / nbytes) * scale))
+
+        def b_dw(ctx, i, c=c):
+            x = ctx.from_numpy(I.normal(10 * i, c["x"]), "float16")
+            w = ctx.from_numpy(I.uniform(10 * i + 1, c["w"], -0.5, 0.5), "float16")
+            b = ctx.from_numpy(np.zeros(c["w"][0], np.float32), "float16")
+            y = ctx.tensor("float16", list(c["y"]))
+            ctx.convolution(x, w, b, list(c["s"]), list(c["p"]), [1, 1], False, [0, 0], c["groups"], y)
+            return ctx.last_kernel
+        k, s, a = measure(W, b_dw, n)
+        rec(f"{v}_depthwise_f16", k, s, a, conv_flops(c), nbytes, "hbm", None)
+        # batched-instance form: one launch over 256 instances
+        ctx = W.Context(0)
+        try:
+            cb = dict(c)
+            xb = (256,) + tuple(c["x"][1:])
+            x = ctx.from_numpy(I.normal(3, xb), "float16")
+            w = ctx.from_numpy(I.uniform(4, c["w"], -0.5, 0.5), "float16")
+            y = ctx.tensor("float16", [256] + list(c["y"][1:]))
+            ctx.convolution(x, w, None, list(c["s"]), list(c["p"]), [1, 1], False, [0, 0], c["groups"], y)
+            ms = time_ctx(ctx, 20)
+        finally:
+            ctx.destroy()
+        bbytes = (int(np.prod(c["x"])) + int(np.prod(c["y"]))) * 2 * 256 + int(np.prod(c["w"])) * 2
+        out[f"{v}_depthwise_f16"]["GBps_batched256"] = bbytes / ms / 1e6
+        out[f"{v}_depthwise_f16"]["frac_of_peak_batched256"] = bbytes / ms / 1e6 / PEAK["hbm_GBps"]
+        log(f"{'':28s} batched x256: {ms*1e3:9.2f} us  {bbytes/ms/1e6:9.1f} GB/s  "
+            f"{100*bbytes/ms/1e6/PEAK['hbm_GBps']:5.1f}% of HBM")
+
+    # config 4: addmm fp16, NN and NT
+    M, K, N = 4096, 768, 3072
+    for tb in (False, True):
+        def b_addmm(ctx, i, tb=tb):
+            x = ctx.from_numpy(I.normal(10 * i, (M, K)), "float16")
+            wshape = (N, K) if tb else (K, N)
+            w = ctx.from_numpy(I.normal(10 * i + 1, wshape, 0, 0.02), "float16")
+            b = ctx.from_numpy(I.uniform(10 * i + 2, (N,), -0.1, 0.1), "float16")
+            o = ctx.tensor("float16", [M, N])
+            ctx.addmm(b, x, w, o, trans_b=tb)
+            return ctx.last_kernel
+        nb = (M * K + K * N + N + M * N) * 2
+        k, s, a = measure(W, b_addmm, max(4, int(9 * scale)), reps_shape=20, reps_amort=3)
+        rec(f"4_addmm_f16_{'NT' if tb else 'NN'}", k, s, a, 2.0 * M * N * K, nb, "mfma", PEAK["fp16_TFLOPs"])
+
+    # config 4: bmm fp16
+    def b_bmm(ctx, i):
+        a = ctx.from_numpy(I.normal(10 * i, (16, 1024, 64)), "float16")
+        b = ctx.from_numpy(I.normal(10 * i + 1, (16, 64, 1024)), "float16")
+        o = ctx.tensor("float16", [16, 1024, 1024])
+        ctx.bmm(a, b, o)
+        return ctx.last_kernel
+    nb = (2 * 16 * 1024 * 64 + 16 * 1024 * 1024) * 2
+    k, s, a = measure(W, b_bmm, max(4, int(9 * scale)), reps_shape=20, reps_amort=3)
+    rec("4_bmm_f16", k, s, a, 2.0 * 16 * 1024 * 1024 * 64, nb, "hbm", None)
+    return out
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(I, budget_s=20.0):
+    """The oracle's WGSL restatement (f32, order-faithful) on this host's
+    cores, over whole steps of the default workload until budget_s is used."""
+    import oracle
+
+    n_thr = oracle.num_threads()
+    data = {}
+    for v, c in CONV2.items():
+        data[v] = (I.uniform(100, c["x"], -1, 1), I.kaiming_uniform(101, c["w"]),
+                   I.uniform(102, (c["w"][0],), -0.1, 0.1))
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        for v, c in CONV2.items():
+            x, w, b = data[v]
+            oracle.emu_conv2d(0, x, w, b, c["s"], c["p"])
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= 50:
+            break
+    flops = sum(conv_flops(c) for c in CONV2.values()) * steps
+    return {"value": flops / el / 1e9, "unit": "GFLOP/s", "cores": n_thr, "kind": "port",
+            "sample": f"{steps} full steps (conv 2a + 2b, float32, batch 1) of the oracle's "
+                      f"order-faithful C restatement of the reference WGSL kernels, "
+                      f"{el:.1f} s on {n_thr} OpenMP threads; Dawn+SwiftShader is unavailable offline"}
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--detail", type=str, default=None, help="write per-config JSON here")
+    ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quick", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on exactly one GPU (the hot path is not sharded); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from __graft_entry__ import load_package
+
+    pkg = load_package()
+    W, I = pkg.wgx, pkg.inputs
+
+    # ---- headline: config 2 (2a + 2b), float32, one submit per step
+    ctx = W.Context(0)
+    kernels = {}
+    for v, c in CONV2.items():
+        kernels[v] = build_conv(ctx, I, c, "float32", 40 + 10 * (v == "2b"))
+    for _ in range(args.warmup):
+        ctx.submit()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.submit()
+    ctx.sync()
+    el = time.perf_counter() - t0
+    ctx.destroy()
+    ms_step = el * 1e3 / args.steps
+    step_flops = sum(conv_flops(c) for c in CONV2.values())
+    value = step_flops / (ms_step * 1e-3) / 1e9
+
+    # ---- dominant kernel: per-launch duration with HIP events on its stream
+    per_kernel = {}
+    for v, c in CONV2.items():
+        kctx = W.Context(0)
+        try:
+            build_conv(kctx, I, c, "float32", 40)
+            per_kernel[v] = time_ctx(kctx, 200)
+        finally:
+            kctx.destroy()
+    dom = max(per_kernel, key=per_kernel.get)
+    dom_ms = per_kernel[dom]
+    achieved = conv_flops(CONV2[dom]) / (dom_ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK["fp32_TFLOPs"],
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK["fp32_TFLOPs"], 4), "traffic": None,
+                "kernel": kernels[dom], "workload": f"conv {dom}",
+                "launch_us": round(dom_ms * 1e3, 2)}
+
+    detail = {}
+    if not args.no_detail:
+        log("---- per-configuration detail (amortised = graph of instances over >= 300 MB)")
+        detail = detail_configs(W, I, quick=args.quick)
+        if args.detail:
+            with open(args.detail, "w") as f:
+                json.dump(detail, f, indent=1)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(I, budget_s=20.0)
+
+    line = {
+        "metric": "mm/conv GFLOP/s & % roofline; depthwise HBM GB/s; YOLO-N-shaped fp16 ms/frame",
+        "value": round(value, 2), "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "aten.convolution im2col-GEMM fp32 NCHW batch 1: "
+                               "[1,64,80,80]*[128,64,3,3] s1p1 + [1,128,80,80]*[256,128,3,3] s2p1",
+                   "kernels": kernels, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    if detail:
+        line["detail"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                              for kk, vv in d.items()} for k, d in detail.items()}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

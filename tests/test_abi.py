@@ -1,0 +1,166 @@
+"""CPU tests of the C-ABI boundary: libwgx.so loads and exports every symbol
+include/wgx.h declares, and the host-only validation context reproduces the
+reference's accept/reject behaviour and integer shape logic without a GPU.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "wgx.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wgx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    L = pkg.wgx.lib()
+    names = declared_symbols()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(pkg.wgx.SIGNATURES), set(names) ^ set(pkg.wgx.SIGNATURES)
+
+
+def test_struct_layouts_match_header(pkg):
+    W = pkg.wgx
+    assert ctypes.sizeof(W.CTensor) == 8 + 4 + 4 + 8 * 8
+    assert ctypes.sizeof(W.CConvArgs) == 4 * 13
+
+
+@pytest.fixture()
+def hctx(pkg):
+    c = pkg.wgx.Context(-1)
+    yield c
+    c.destroy()
+
+
+def test_host_context_buffers(hctx):
+    assert not hctx.has_device and hctx.arch == "host"
+    p = hctx.storage_buffer(1)
+    assert hctx.buffer_size(p) == 4  # max(4, round_up(size, 4)), src/context.ts:86-92
+    t = hctx.tensor("float32", [2, 3])
+    assert t.byte_length == 24 and t.numel == 6
+    t.set_data(np.arange(6, dtype=np.float32))
+    t.set_data(np.array([7, 8], np.float32))
+    assert t.get_data().ravel().tolist() == [7, 8, 2, 3, 4, 5]
+    with pytest.raises(ValueError, match="pass a view"):
+        t.set_data(np.zeros(8, np.float32))
+    with pytest.raises(ValueError, match="exceeds maximum rank"):
+        hctx.tensor("float32", [1] * 9)
+    with pytest.raises(ValueError, match="positive integers"):
+        hctx.tensor("float32", [0, 3])
+    with pytest.raises(ValueError, match="< required"):
+        hctx.tensor("float32", [4, 4], buffer=hctx.storage_buffer(16))
+
+
+def test_submit_without_device_fails_loudly(hctx, pkg):
+    a, b, o = hctx.tensor("float32", [4, 4]), hctx.tensor("float32", [4, 4]), hctx.tensor("float32", [4, 4])
+    hctx.mm(a, b, o)
+    with pytest.raises(pkg.wgx.WgxError, match="no device"):
+        hctx.submit()
+
+
+def test_mm_validation(hctx, pkg):
+    E = pkg.wgx.WgxError
+    a = hctx.tensor("float32", [4, 8])
+    b = hctx.tensor("float32", [8, 5])
+    o = hctx.tensor("float32", [4, 5])
+    hctx.mm(a, b, o)
+    assert hctx.last_kernel.startswith("gemm_f32")
+    with pytest.raises(E, match="inner dimensions must match"):
+        hctx.mm(a, a, o)
+    with pytest.raises(E, match="Output shape|output shape"):
+        hctx.mm(a, b, hctx.tensor("float32", [5, 4]))
+    with pytest.raises(E, match="2D"):
+        hctx.mm(hctx.tensor("float32", [1, 4, 8]), b, o)
+    with pytest.raises(E, match="matching"):
+        hctx.mm(hctx.tensor("float16", [4, 8]), b, o)
+    h = [hctx.tensor("float16", s) for s in ([64, 96], [96, 80], [64, 80])]
+    hctx.mm(*h)
+    assert hctx.last_kernel.startswith("gemm_mfma_f16") and hctx.last_kernel.endswith("kn")
+    hctx.mm(h[0], hctx.tensor("float16", [80, 96]), h[2], trans_b=True)
+    assert hctx.last_kernel.endswith("nk")
+    with pytest.raises(E, match="bias"):
+        hctx.mm(*h, bias=hctx.tensor("float16", [7]))
+
+
+def test_buffer_bounds_are_enforced(hctx, pkg):
+    """A view larger than its buffer never reaches a launch record."""
+    W = pkg.wgx
+    small = hctx.storage_buffer(64)
+    t = W.Tensor(hctx, "float32", [16], small, 64)
+    big = W.Tensor.__new__(W.Tensor)
+    big.ctx, big.dtype, big.shape, big.ptr = hctx, "float32", [32], small
+    big.numel, big.byte_length = 32, 128
+    with pytest.raises(W.WgxError, match="not inside a buffer"):
+        hctx.mm(big.__class__.__new__(W.Tensor) if False else big, t, t)
+
+
+def test_conv_validation_and_variants(hctx, pkg):
+    E = pkg.wgx.WgxError
+    T = hctx.tensor
+
+    def conv(xs, ws, os_, stride=(1, 1), pad=(0, 0), dil=(1, 1), groups=1, transposed=False,
+             op=(0, 0), dtype="float16", bias=True):
+        x, w, y = T(dtype, xs), T(dtype, ws), T(dtype, os_)
+        b = T(dtype, [os_[1]]) if bias else None
+        hctx.convolution(x, w, b, stride, pad, dil, transposed, op, groups, y)
+        return hctx.last_kernel
+
+    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)).endswith("_conv")
+    assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)).endswith("_conv")
+    assert conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8]).endswith("_kn")
+    assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3"
+    assert conv([1, 512, 20, 20], [512, 1, 5, 5], [1, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5"
+    assert conv([1, 8, 10, 10], [12, 4, 3, 3], [1, 12, 10, 10], pad=(1, 1), groups=2) == "conv_grouped_direct"
+    assert conv([1, 2, 3, 3], [2, 2, 3, 3], [1, 2, 6, 6], (2, 2), (1, 1), transposed=True, op=(1, 1)) == "conv_transpose_direct"
+    assert conv([1, 3, 64, 64], [16, 3, 3, 3], [1, 16, 32, 32], (2, 2), (1, 1), dtype="float32").startswith("gemm_f32")
+    # the reference's output-size rule, floor((I + 2p - d(K-1) - 1) / s) + 1
+    with pytest.raises(E, match=r"expected output spatial \[3, 3\]"):
+        conv([1, 2, 5, 5], [3, 2, 3, 3], [1, 3, 2, 2], (2, 2), (1, 1))
+    with pytest.raises(E, match=r"expected output spatial \[6, 6\]"):
+        conv([1, 2, 3, 3], [2, 2, 3, 3], [1, 2, 5, 5], (2, 2), (1, 1), transposed=True, op=(1, 1))
+    with pytest.raises(E, match="weight in-ch"):
+        conv([1, 4, 8, 8], [8, 3, 3, 3], [1, 8, 6, 6])
+    with pytest.raises(E, match="output_padding"):
+        conv([1, 4, 8, 8], [8, 4, 3, 3], [1, 8, 6, 6], op=(1, 0))
+    with pytest.raises(E, match="kernel larger than input"):
+        conv([1, 4, 2, 2], [8, 4, 5, 5], [1, 8, 1, 1])
+    with pytest.raises(E, match="output_padding >= stride"):
+        conv([1, 2, 3, 3], [2, 2, 3, 3], [1, 2, 7, 7], (2, 2), (1, 1), transposed=True, op=(2, 2))
+    with pytest.raises(E, match="4D"):
+        conv([1, 4, 8], [8, 4, 3, 3], [1, 8, 6, 6])
+    with pytest.raises(E, match="matching float32 or float16"):
+        conv([1, 4, 8, 8], [8, 4, 3, 3], [1, 8, 6, 6], dtype="bfloat16")
+
+
+def test_im2col_table_matches_oracle_indexing(pkg, orc):
+    """The k -> (offset, tap) rule the conv kernels use reproduces im2col
+    exactly (gathered on the CPU here and multiplied in float64)."""
+    I = pkg.inputs
+    x = I.uniform(1, (1, 5, 9, 11), -1, 1)
+    w = I.uniform(2, (4, 5, 3, 2), -1, 1)
+    s, p, d = (2, 1), (1, 2), (2, 1)
+    y, _ = orc.conv2d_f64(x, w, None, s, p, d)
+    IC, IH, IW, KH, KW = 5, 9, 11, 3, 2
+    OH, OW = y.shape[2:]
+    K = IC * KH * KW
+    cols = np.zeros((K, OH * OW))
+    for k in range(K):
+        ic, tap = divmod(k, KH * KW)
+        kh, kw = divmod(tap, KW)
+        off = ic * IH * IW + kh * d[0] * IW + kw * d[1]
+        for n in range(OH * OW):
+            oh, ow = divmod(n, OW)
+            ih0, iw0 = oh * s[0] - p[0], ow * s[1] - p[1]
+            ih, iw = ih0 + kh * d[0], iw0 + kw * d[1]
+            if 0 <= ih < IH and 0 <= iw < IW:
+                cols[k, n] = x.ravel()[ih0 * IW + iw0 + off]
+    got = w.reshape(4, K).astype(np.float64) @ cols
+    assert np.max(np.abs(got - y.reshape(4, -1))) < 1e-12

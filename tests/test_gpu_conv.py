@@ -1,0 +1,144 @@
+"""GPU parity for aten.convolution (implicit-im2col GEMM, 1x1, depthwise,
+grouped and transposed fallbacks) and the conv_with_clamp epilogue, through
+the C-ABI.  Reference behaviour: src/shaders/convolution/index.ts:58-310.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import assert_parity, normwise, round_in
+
+pytestmark = pytest.mark.gpu
+
+
+def _arr(t):
+    return np.asarray(t["data"], np.float32).reshape(t["shape"])
+
+
+def run_conv(ctx, x, w, b, dtype, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1,
+             transposed=False, output_padding=(0, 0), out_shape=None, clamp=None):
+    tx, tw = ctx.from_numpy(x, dtype), ctx.from_numpy(w, dtype)
+    tb = ctx.from_numpy(b, dtype) if b is not None else None
+    ty = ctx.tensor(dtype, out_shape)
+    ctx.reset()
+    ctx.convolution(tx, tw, tb, list(stride), list(padding), list(dilation), transposed,
+                    list(output_padding), groups, ty, clamp=clamp)
+    kernel = ctx.last_kernel
+    ctx.submit()
+    ctx.sync()
+    return ty.get_f32(), kernel
+
+
+def test_reference_kats_conv(gpu_ctx, kats):
+    for c in kats:
+        if c["op"] != "aten.convolution.default":
+            continue
+        dt = c["dtype"]
+        x, w = round_in(_arr(c["input"]), dt), round_in(_arr(c["weight"]), dt)
+        b = round_in(_arr(c["bias"]), dt) if c["bias"] else None
+        got, kernel = run_conv(gpu_ctx, x, w, b, dt, c["stride"], c["padding"], c["dilation"],
+                               c["groups"], c["transposed"], c["output_padding"], c["out_shape"])
+        if c["expected"] is not None:
+            err = np.max(np.abs(got.ravel() - np.asarray(c["expected"])))
+            assert err <= max(c["tol"], 2e-5), f"{c['source']} via {kernel}: {err}"
+        else:  # element-0 checks of the 1x1 tile tests
+            e0 = float(np.dot(x.reshape(x.shape[1], -1)[:, 0].astype(np.float64),
+                              w.reshape(w.shape[0], -1)[0].astype(np.float64)))
+            assert abs(got.ravel()[0] - e0) <= c["tol"], c["source"]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+@pytest.mark.parametrize("variant", ["2a", "2b"])
+def test_config2_conv(gpu_ctx, orc, pkg, dtype, variant):
+    I = pkg.inputs
+    if variant == "2a":
+        xs, ws, s, os_ = (1, 64, 80, 80), (128, 64, 3, 3), (1, 1), [1, 128, 80, 80]
+    else:
+        xs, ws, s, os_ = (1, 128, 80, 80), (256, 128, 3, 3), (2, 2), [1, 256, 40, 40]
+    x = round_in(I.uniform(40, xs, -1, 1), dtype)
+    w = round_in(I.kaiming_uniform(41, ws), dtype)
+    b = round_in(I.uniform(42, (ws[0],), -0.1, 0.1), dtype)
+    got, kernel = run_conv(gpu_ctx, x, w, b, dtype, s, (1, 1), out_shape=os_)
+    ref, refa = orc.conv2d_f64(x, w, b, s, (1, 1))
+    K = ws[1] * ws[2] * ws[3]
+    assert_parity(got, ref, refa, dtype, K, f"config{variant} {dtype} {kernel}")
+    if dtype == "float16":
+        emu = orc.emu_conv2d(1, x, w, b, s, (1, 1))
+        assert normwise(got, emu) < 2e-2
+
+
+@pytest.mark.parametrize("case", ["A", "B"])
+def test_config3_depthwise_fp16(gpu_ctx, orc, pkg, case):
+    I = pkg.inputs
+    if case == "A":
+        xs, ws, s, p, os_ = (1, 256, 40, 40), (256, 1, 3, 3), (1, 1), (1, 1), [1, 256, 40, 40]
+    else:
+        xs, ws, s, p, os_ = (1, 512, 20, 20), (512, 1, 5, 5), (2, 2), (2, 2), [1, 512, 10, 10]
+    x = I.as_f16(I.normal(50, xs))
+    w = I.as_f16(I.uniform(51, ws, -0.5, 0.5))
+    b = np.zeros(ws[0], np.float32)
+    got, kernel = run_conv(gpu_ctx, x, w, b, "float16", s, p, groups=ws[0], out_shape=os_)
+    assert kernel.startswith("depthwise"), kernel
+    ref, refa = orc.conv2d_f64(x, w, b, s, p, groups=ws[0])
+    assert_parity(got, ref, refa, "float16", ws[2] * ws[3], f"config3{case} {kernel}")
+    emu = orc.emu_conv2d(1, x, w, b, s, p, groups=ws[0])
+    assert normwise(got, emu) < 1e-2
+
+
+CONV_SWEEP = [
+    # x shape, w shape, stride, pad, dilation, groups
+    ((1, 3, 64, 64), (16, 3, 3, 3), (2, 2), (1, 1), (1, 1), 1),      # stem: K = 27
+    ((1, 32, 20, 20), (64, 32, 1, 1), (1, 1), (0, 0), (1, 1), 1),    # pointwise
+    ((2, 32, 17, 19), (48, 32, 1, 1), (1, 1), (0, 0), (1, 1), 1),    # pointwise, batch 2, ragged
+    ((1, 16, 21, 13), (24, 16, 1, 1), (2, 2), (0, 0), (1, 1), 1),    # strided 1x1 -> im2col path
+    ((2, 24, 15, 15), (40, 24, 3, 3), (1, 1), (2, 2), (2, 2), 1),    # dilation 2
+    ((1, 16, 33, 31), (72, 16, 5, 5), (2, 1), (2, 1), (1, 1), 1),    # 5x5, mixed stride/pad
+    ((1, 8, 9, 9), (8, 8, 7, 7), (1, 1), (3, 3), (1, 1), 1),         # 7x7 (49 taps)
+    ((1, 64, 8, 8), (300, 64, 3, 3), (1, 1), (1, 1), (1, 1), 1),     # OC not a tile multiple
+    ((2, 16, 12, 12), (16, 1, 3, 3), (1, 1), (1, 1), (1, 1), 16),    # depthwise, batch 2
+    ((1, 12, 19, 23), (12, 1, 7, 7), (2, 3), (3, 2), (1, 2), 12),    # depthwise generic
+    ((1, 8, 10, 10), (12, 4, 3, 3), (1, 1), (1, 1), (1, 1), 2),      # grouped fallback
+    ((1, 3, 70, 70), (8, 3, 4, 4), (3, 3), (0, 0), (1, 1), 1),       # no padding, K = 48
+]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_conv_sweep(gpu_ctx, orc, pkg, dtype):
+    I = pkg.inputs
+    for i, (xs, ws, s, p, d, g) in enumerate(CONV_SWEEP):
+        x = round_in(I.uniform(500 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(600 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(700 + i, (ws[0],), -0.5, 0.5), dtype) if i % 3 else None
+        ref, refa = orc.conv2d_f64(x, w, b, s, p, d, g)
+        got, kernel = run_conv(gpu_ctx, x, w, b, dtype, s, p, d, g, out_shape=list(ref.shape))
+        K = ws[1] * ws[2] * ws[3]
+        assert_parity(got, ref, refa, dtype, K, f"sweep {i} {dtype} {xs}x{ws} s{s} p{p} d{d} g{g} {kernel}")
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_conv_transpose(gpu_ctx, orc, pkg, dtype):
+    I = pkg.inputs
+    for i, (xs, ws, s, p, d, g, op) in enumerate([
+        ((1, 4, 7, 6), (4, 3, 3, 3), (2, 2), (1, 1), (1, 1), 1, (1, 1)),
+        ((2, 6, 5, 5), (6, 2, 2, 3), (2, 1), (0, 1), (1, 2), 3, (1, 0)),
+    ]):
+        x = round_in(I.uniform(800 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(810 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(820 + i, (ws[1] * g,), -0.5, 0.5), dtype)
+        ref, refa = orc.conv_transpose2d_f64(x, w, b, s, p, d, g, op)
+        got, kernel = run_conv(gpu_ctx, x, w, b, dtype, s, p, d, g, True, op, list(ref.shape))
+        assert_parity(got, ref, refa, dtype, xs[1] // g * ws[2] * ws[3], f"convT {i} {dtype} {kernel}")
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_conv_with_clamp_epilogue(gpu_ctx, orc, pkg, dtype):
+    """et_vk.conv_with_clamp: bias, then clamp, then one rounding."""
+    I = pkg.inputs
+    for xs, ws, g in (((1, 16, 12, 12), (32, 16, 3, 3), 1), ((1, 16, 12, 12), (16, 1, 3, 3), 16)):
+        x = round_in(I.uniform(900, xs, -1, 1), dtype)
+        w = round_in(I.uniform(901, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(902, (ws[0],), -0.5, 0.5), dtype)
+        ref, refa = orc.conv2d_f64(x, w, b, (1, 1), (1, 1), groups=g)
+        got, kernel = run_conv(gpu_ctx, x, w, b, dtype, (1, 1), (1, 1), groups=g,
+                               out_shape=list(ref.shape), clamp=(0.0, 6.0))
+        assert got.min() >= 0.0 and got.max() <= 6.0
+        assert_parity(got, np.clip(ref, 0.0, 6.0), refa, dtype, ws[1] * 9, f"clamp {kernel}")

@@ -1,0 +1,141 @@
+"""GPU parity for aten.mm / aten.addmm / aten.bmm through the C-ABI.
+
+Reference behaviour: src/shaders/mm/index.ts:32-93, src/shaders/bmm/
+index.ts:27-96; addmm is the reference's mm + broadcast add composition.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import assert_parity, normwise, round_in, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _arr(t):
+    return np.asarray(t["data"], np.float32).reshape(t["shape"])
+
+
+def run_mm(ctx, A, B, dtype, bias=None, trans_b=False, alpha=1.0, beta=1.0):
+    ta, tb = ctx.from_numpy(A, dtype), ctx.from_numpy(B, dtype)
+    M, N = A.shape[0], (B.shape[0] if trans_b else B.shape[1])
+    to = ctx.tensor(dtype, [M, N])
+    tbias = ctx.from_numpy(bias, dtype) if bias is not None else None
+    ctx.reset()
+    ctx.mm(ta, tb, to, bias=tbias, alpha=alpha, beta=beta, trans_b=trans_b)
+    kernel = ctx.last_kernel
+    ctx.submit()
+    ctx.sync()
+    return to.get_f32(), kernel
+
+
+def test_reference_kats_mm_bmm(gpu_ctx, kats):
+    for c in kats:
+        if c["op"] not in ("aten.mm.default", "aten.bmm.default"):
+            continue
+        a, b = round_in(_arr(c["a"]), c["dtype"]), round_in(_arr(c["b"]), c["dtype"])
+        ta, tb = gpu_ctx.from_numpy(a, c["dtype"]), gpu_ctx.from_numpy(b, c["dtype"])
+        shape = list(a.shape[:-1]) + [b.shape[-1]]
+        to = gpu_ctx.tensor(c["dtype"], shape)
+        gpu_ctx.reset()
+        if c["op"] == "aten.mm.default":
+            gpu_ctx.mm(ta, tb, to)
+        else:
+            gpu_ctx.bmm(ta, tb, to)
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        got = to.get_f32()
+        exp = np.matmul(a.astype(np.float64), b.astype(np.float64))
+        if c["expected"] is not None:
+            assert np.max(np.abs(got.ravel() - np.asarray(c["expected"]))) <= c["tol"], c["source"]
+        assert np.max(np.abs(got - exp)) <= c["tol"], c["source"]
+
+
+def test_config1_mm_fp32_512(gpu_ctx, orc, pkg):
+    I = pkg.inputs
+    A = I.uniform(0, (512, 512), -1, 1)
+    B = I.uniform(1, (512, 512), -1, 1)
+    got, kernel = run_mm(gpu_ctx, A, B, "float32")
+    ref, refa = orc.gemm_f64(A, B)
+    assert_parity(got, ref, refa, "float32", 512, "config1 " + kernel)
+    emu = orc.emu_gemm(0, A, B)
+    assert normwise(got, emu) < 1e-6
+
+
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_config4_addmm_fp16(gpu_ctx, orc, pkg, trans_b):
+    I = pkg.inputs
+    X = I.as_f16(I.normal(10, (4096, 768)))
+    W = I.as_f16(I.normal(11, (768, 3072), 0.0, 0.02))
+    bias = I.as_f16(I.uniform(12, (3072,), -0.1, 0.1))
+    Wop = np.ascontiguousarray(W.T) if trans_b else W
+    got, kernel = run_mm(gpu_ctx, X, Wop, "float16", bias=bias, trans_b=trans_b)
+    rows = sample_rows(4096)
+    ref, refa = orc.gemm_f64(X, W, bias, rows=rows)
+    assert_parity(got[rows], ref, refa, "float16", 768, "config4 addmm " + kernel)
+    emu = orc.emu_addmm(1, X, W, bias, rows=rows[:64])
+    assert normwise(got[rows[:64]], emu) < 2e-2
+
+
+def test_config4_addmm_nn_equals_nt_bitwise(gpu_ctx, pkg):
+    """Both weight layouts feed identical k-ordered fragments to the MFMA."""
+    I = pkg.inputs
+    X = I.as_f16(I.normal(20, (512, 768)))
+    W = I.as_f16(I.normal(21, (768, 384), 0.0, 0.02))
+    bias = I.as_f16(I.uniform(22, (384,), -0.1, 0.1))
+    nn, _ = run_mm(gpu_ctx, X, W, "float16", bias=bias)
+    nt, _ = run_mm(gpu_ctx, X, np.ascontiguousarray(W.T), "float16", bias=bias, trans_b=True)
+    assert np.array_equal(nn.view(np.uint32), nt.view(np.uint32))
+
+
+def test_config4_bmm_fp16(gpu_ctx, orc, pkg):
+    I = pkg.inputs
+    A = I.as_f16(I.normal(30, (16, 1024, 64)))
+    B = I.as_f16(I.normal(31, (16, 64, 1024)))
+    ta, tb = gpu_ctx.from_numpy(A, "float16"), gpu_ctx.from_numpy(B, "float16")
+    to = gpu_ctx.tensor("float16", [16, 1024, 1024])
+    gpu_ctx.reset()
+    gpu_ctx.bmm(ta, tb, to)
+    kernel = gpu_ctx.last_kernel
+    gpu_ctx.submit()
+    gpu_ctx.sync()
+    got = to.get_f32()
+    ref, refa = orc.gemm_f64(A, B)
+    assert_parity(got, ref, refa, "float16", 64, "bmm " + kernel)
+
+
+SHAPES = [(5, 3, 7), (1, 1, 1), (33, 65, 17), (64, 64, 64), (100, 37, 129), (130, 260, 72),
+          (257, 129, 200), (96, 1000, 8), (7, 300, 513)]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_mm_shapes_sweep(gpu_ctx, orc, pkg, dtype, trans_b):
+    I = pkg.inputs
+    for i, (M, N, K) in enumerate(SHAPES):
+        A = round_in(I.uniform(100 + i, (M, K), -1, 1), dtype)
+        B = round_in(I.uniform(200 + i, (K, N), -1, 1), dtype)
+        bias = round_in(I.uniform(300 + i, (N,), -0.5, 0.5), dtype)
+        Bop = np.ascontiguousarray(B.T) if trans_b else B
+        alpha, beta = (0.5, 2.0) if i % 2 else (1.0, 1.0)
+        got, kernel = run_mm(gpu_ctx, A, Bop, dtype, bias=bias, trans_b=trans_b, alpha=alpha, beta=beta)
+        ref, refa = orc.gemm_f64(A, B)
+        ref = alpha * ref + beta * bias
+        refa = abs(alpha) * refa + abs(beta) * np.abs(bias)
+        assert_parity(got, ref, refa, dtype, K, f"mm {dtype} {M}x{N}x{K} tb={trans_b} {kernel}")
+
+
+def test_bmm_trans_and_ragged(gpu_ctx, orc, pkg):
+    I = pkg.inputs
+    for dtype in ("float32", "float16"):
+        A = round_in(I.uniform(400, (3, 45, 70), -1, 1), dtype)
+        B = round_in(I.uniform(401, (3, 70, 33), -1, 1), dtype)
+        for tb in (False, True):
+            Bop = np.ascontiguousarray(B.transpose(0, 2, 1)) if tb else B
+            ta, tbb = gpu_ctx.from_numpy(A, dtype), gpu_ctx.from_numpy(Bop, dtype)
+            to = gpu_ctx.tensor(dtype, [3, 45, 33])
+            gpu_ctx.reset()
+            gpu_ctx.bmm(ta, tbb, to, trans_b=tb)
+            gpu_ctx.submit()
+            gpu_ctx.sync()
+            ref, refa = orc.gemm_f64(A, B)
+            assert_parity(to.get_f32(), ref, refa, dtype, 70, f"bmm {dtype} tb={tb}")

@@ -1,0 +1,117 @@
+"""GPU tests of the execution model: submit/sync/reset semantics, copies,
+setData prefixes and graph replays (src/context.ts:172-389, src/tensor.ts:149-192).
+"""
+import numpy as np
+import pytest
+
+from gpu_util import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def test_copy_and_prefix_write(pkg):
+    W = pkg.wgx
+    ctx = W.Context(0)
+    try:
+        src = ctx.tensor("float32", [4]).set_data(np.array([1, 2, 3, 4], np.float32))
+        dst = ctx.tensor("float32", [4])
+        ctx.copy(src, dst)
+        ctx.submit()
+        ctx.sync()
+        assert dst.get_data().tolist() == [1, 2, 3, 4]
+        t = ctx.tensor("float32", [2, 3]).set_data(np.arange(1, 7, dtype=np.float32))
+        t.set_data(np.array([7, 8], np.float32))
+        assert t.get_data().ravel().tolist() == [7, 8, 3, 4, 5, 6]
+        u = ctx.tensor("uint8", [3]).set_data(np.array([7, 42, 99], np.uint8))
+        assert u.get_data().tolist() == [7, 42, 99]
+        ctx.reset()
+        ctx.submit()  # empty: no-op
+        ctx.sync()
+    finally:
+        ctx.destroy()
+
+
+def test_graph_replays_match_eager(pkg, orc):
+    """Every replay of the captured graph equals the eager launch sequence,
+    with eager work and synchronisations between the replays."""
+    W, I = pkg.wgx, pkg.inputs
+    results = {}
+    for graph in (False, True):
+        ctx = W.Context(0)
+        try:
+            ctx.set_graph_mode(graph)
+            x = I.as_f16(I.uniform(1, (1, 32, 24, 24), -1, 1))
+            w1 = I.as_f16(I.kaiming_uniform(2, (64, 32, 3, 3)))
+            w2 = I.as_f16(I.uniform(3, (64, 1, 3, 3), -0.5, 0.5))
+            tx, t1, t2 = (ctx.from_numpy(a, "float16") for a in (x, w1, w2))
+            y1 = ctx.tensor("float16", [1, 64, 24, 24])
+            y2 = ctx.tensor("float16", [1, 64, 24, 24])
+            y3 = ctx.tensor("float16", [1, 64, 24, 24])
+            ctx.convolution(tx, t1, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 1, y1)
+            ctx.unary("sigmoid", y1, y2)
+            ctx.mul(y1, y2, y2)
+            ctx.convolution(y2, t2, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 64, y3)
+            outs = []
+            for rep in range(4):
+                ctx.submit()
+                ctx.sync()
+                outs.append(y3.get_data().copy())
+                # eager work in between: overwrite the intermediate, then replay again
+                y1.set_data(np.zeros((1, 64, 24, 24), np.float16))
+            for o in outs[1:]:
+                assert np.array_equal(o.view(np.uint16), outs[0].view(np.uint16))
+            results[graph] = outs[0]
+        finally:
+            ctx.destroy()
+    assert np.array_equal(results[True].view(np.uint16), results[False].view(np.uint16))
+
+
+def test_time_submits_positive(pkg):
+    W, I = pkg.wgx, pkg.inputs
+    ctx = W.Context(0)
+    try:
+        a = ctx.from_numpy(I.uniform(1, (256, 256), -1, 1), "float16")
+        b = ctx.from_numpy(I.uniform(2, (256, 256), -1, 1), "float16")
+        o = ctx.tensor("float16", [256, 256])
+        ctx.mm(a, b, o)
+        ms = ctx.time_submits(10)
+        assert 0.0 < ms < 100.0
+    finally:
+        ctx.destroy()
+
+
+def test_elementwise_ops(pkg, orc):
+    W, I = pkg.wgx, pkg.inputs
+    ctx = W.Context(0)
+    try:
+        a = I.as_f16(I.uniform(10, (2, 3, 4, 5), -3, 3))
+        b = I.as_f16(I.uniform(11, (1, 3, 1, 5), -3, 3))
+        ta, tb = ctx.from_numpy(a, "float16"), ctx.from_numpy(b, "float16")
+        o_add, o_mul, o_sig = (ctx.tensor("float16", [2, 3, 4, 5]) for _ in range(3))
+        ctx.add(ta, tb, o_add, alpha=2.0)
+        ctx.mul(ta, tb, o_mul)
+        ctx.unary("sigmoid", ta, o_sig)
+        c1 = ctx.tensor("float16", [2, 3, 4, 5])
+        c2 = ctx.tensor("float16", [2, 2, 4, 5])
+        cat = ctx.tensor("float16", [2, 5, 4, 5])
+        ctx.copy(o_add, c1)
+        ctx.split(ta, 1, [ctx.tensor("float16", [2, 1, 4, 5]), c2])
+        ctx.cat([c1, c2], 1, cat)
+        up = ctx.tensor("float16", [2, 3, 8, 10])
+        ctx.upsample_nearest2d(ta, up)
+        mp = ctx.tensor("float16", [2, 3, 4, 5])
+        ctx.max_pool2d(ta, [5, 5], [1, 1], [2, 2], [1, 1], mp)
+        ctx.submit()
+        ctx.sync()
+        ad = a.astype(np.float64)
+        bd = b.astype(np.float64)
+        np.testing.assert_allclose(o_add.get_f32(), ad + 2 * bd, atol=1e-2)
+        np.testing.assert_allclose(o_mul.get_f32(), ad * bd, rtol=1e-3, atol=1e-3)
+        np.testing.assert_allclose(o_sig.get_f32(), 1 / (1 + np.exp(-ad)), atol=2e-3)
+        np.testing.assert_allclose(cat.get_f32(), np.concatenate([o_add.get_f32(), a[:, 1:]], 1))
+        np.testing.assert_array_equal(up.get_f32(), a.repeat(2, 2).repeat(2, 3))
+        pad = np.pad(ad, ((0, 0), (0, 0), (2, 2), (2, 2)), constant_values=-np.inf)
+        ref = np.max(np.stack([pad[:, :, i:i + 4, j:j + 5] for i in range(5) for j in range(5)]), 0)
+        np.testing.assert_array_equal(mp.get_f32(), ref)
+    finally:
+        ctx.destroy()

@@ -1,0 +1,119 @@
+// internal.h -- shared declarations between the runtime and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "wgx.h"
+
+namespace wgx {
+
+// Passing this stream to a launch_* function selects the kernel, fills *name
+// and performs one-time kernel set-up (LDS attributes) without launching.
+inline hipStream_t describe_only() { return reinterpret_cast<hipStream_t>(~uintptr_t(0)); }
+// Like describe_only() but with no HIP call at all (host-only contexts).
+inline hipStream_t name_only() { return reinterpret_cast<hipStream_t>(~uintptr_t(1)); }
+inline bool is_dry(hipStream_t s) { return s == describe_only() || s == name_only(); }
+
+// One GEMM-shaped launch: C[b] = epilogue(A[b] (M x K) * B[b] (K x N)).
+//   A: row-major, k-contiguous, leading dim lda, batch stride sA (0 = shared).
+//   B: bmode NK  -> row-major [N,K] (k-contiguous), leading dim ldb
+//      bmode KN  -> row-major [K,N] (n-contiguous), leading dim ldb
+//      bmode CONV-> implicit im2col of an NCHW input (see ConvGeom): element
+//                   (k, n) = x[b][ktab[k].off + colbase(n)] when tap ktab[k].tap
+//                   is inside the image for output pixel n, else 0.
+//   C: row-major, leading dim ldc, batch stride sC.
+//   epilogue: v = alpha*acc + beta*bias (bias per column n, or per row m),
+//             optional clamp, rounded once to the storage dtype.
+enum BMode { B_NK = 0, B_KN = 1, B_CONV = 2 };
+enum BiasMode { BIAS_NONE = 0, BIAS_COL = 1, BIAS_ROW = 2 };
+
+struct ConvGeom {
+  int IH, IW, OW, sH, sW, pH, pW, KH, KW, dH, dW;
+};
+
+struct GemmDesc {
+  int dtype;  // WGX_FLOAT32 / WGX_FLOAT16 / WGX_BFLOAT16
+  int batch, M, N, K;
+  const void* A;
+  long long lda, sA;
+  const void* B;
+  long long ldb, sB;
+  void* C;
+  long long ldc, sC;
+  const void* bias;
+  int bias_mode;
+  float alpha, beta;
+  int has_clamp;
+  float cmin, cmax;
+  int bmode;
+  ConvGeom g;
+  const int2* ktab;  // device table for B_CONV, Kpad entries {off, tap}
+};
+
+// Table rows needed for a B_CONV launch (K rounded up to the largest K tile).
+int conv_ktab_rows(int K);
+// Fills a host table for B_CONV: entry k = {ic*IH*IW + kh*dH*IW + kw*dW, kh*KW+kw};
+// padding entries get tap 63 (never inside the image).
+void conv_fill_ktab(int2* tab, int K, int IC, const ConvGeom& g);
+
+hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name);
+hipError_t launch_gemm_f32(const GemmDesc& d, hipStream_t s, std::string* name);
+
+struct DwDesc {
+  int dtype;
+  int B, C, IH, IW, OH, OW, KH, KW, sH, sW, pH, pW, dH, dW;
+  const void* x;
+  const void* w;
+  const void* bias;
+  void* y;
+  int has_clamp;
+  float cmin, cmax;
+};
+hipError_t launch_depthwise(const DwDesc& d, hipStream_t s, std::string* name);
+
+struct DirectConvDesc {
+  int dtype;
+  int transposed;
+  int B, IC, IH, IW, OC, OH, OW, KH, KW, sH, sW, pH, pW, dH, dW, groups;
+  const void* x;
+  const void* w;
+  const void* bias;
+  void* y;
+  int has_clamp;
+  float cmin, cmax;
+};
+hipError_t launch_direct_conv(const DirectConvDesc& d, hipStream_t s, std::string* name);
+
+// Elementwise family (eltwise.hip).
+struct BcastDesc {
+  int dtype;
+  int ndim;
+  long long numel;
+  long long out_shape[WGX_MAX_NDIM];
+  long long a_stride[WGX_MAX_NDIM];  // 0 on broadcast dims
+  long long b_stride[WGX_MAX_NDIM];
+  const void* a;
+  const void* b;
+  void* out;
+  float alpha;
+  int op;  // 0 add (a + alpha*b), 1 mul
+};
+hipError_t launch_binary(const BcastDesc& d, hipStream_t s, std::string* name);
+hipError_t launch_unary(int op, int dtype, long long n, const void* x, void* y, hipStream_t s,
+                        std::string* name);
+// Copies a [outer, inner_src] strided block into dst at a column offset:
+// dst[o*inner_dst + off + i] = src[o*inner_src + i], elements of elsize bytes.
+hipError_t launch_slab_copy(int elsize, long long outer, long long inner_src,
+                            long long inner_dst, long long dst_off, long long src_off,
+                            const void* src, void* dst, bool gather, hipStream_t s,
+                            std::string* name);
+hipError_t launch_upsample_nearest(int dtype, int BC, int IH, int IW, int OH, int OW,
+                                   const void* x, void* y, hipStream_t s, std::string* name);
+hipError_t launch_max_pool(int dtype, int BC, int IH, int IW, int OH, int OW, int KH, int KW,
+                           int sH, int sW, int pH, int pW, int dH, int dW, const void* x,
+                           void* y, hipStream_t s, std::string* name);
+
+}  // namespace wgx

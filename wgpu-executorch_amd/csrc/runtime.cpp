@@ -1,0 +1,850 @@
+// runtime.cpp -- the C-ABI of libwgx (include/wgx.h): contexts, owned device
+// buffers, validated launch records, replay through a captured HIP graph.
+//
+// Mirrors WgpuExecutionContext (src/context.ts:17-390): buffers are owned by
+// the context (storageBuffer / #ownedBuffers, context.ts:43-45,86-92),
+// recordShader only validates and appends a command (context.ts:158-161,
+// 201-205), submit replays the whole list in order (context.ts:323-370), sync
+// waits (context.ts:377-380), reset drops the list (context.ts:386-389).
+//
+// MI355X-specific choices:
+//  * one HIP stream per context; the command list is captured once into a
+//    hipGraph and replayed with a single hipGraphLaunch per submit (re-captured
+//    only when the list changes), so a ~300-launch program costs one submit;
+//  * every tensor a record names must lie inside a buffer this context owns,
+//    and its byte extent is checked against that buffer, so no recorded launch
+//    can address memory outside the inputs and outputs it was given;
+//  * implicit-im2col launches get their per-k {offset, tap} table built on
+//    the host at record time (it depends only on shapes) and kept in a
+//    context-owned device buffer.
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <functional>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+using namespace wgx;
+
+namespace {
+
+struct Buf {
+  uint64_t size;
+  uint32_t usage;
+};
+
+struct Cmd {
+  std::function<hipError_t(hipStream_t)> fn;
+  std::string name;
+};
+
+int elsize(int dt) {
+  switch (dt) {
+    case WGX_FLOAT32:
+    case WGX_INT32:
+      return 4;
+    case WGX_FLOAT16:
+    case WGX_BFLOAT16:
+      return 2;
+    case WGX_INT8:
+    case WGX_UINT8:
+    case WGX_BOOL:
+      return 1;
+    case WGX_FLOAT64:
+    case WGX_INT64:
+      return 8;
+    default:
+      return 0;
+  }
+}
+
+const char* dtname(int dt) {
+  switch (dt) {
+    case WGX_FLOAT32: return "float32";
+    case WGX_FLOAT16: return "float16";
+    case WGX_BFLOAT16: return "bfloat16";
+    case WGX_INT32: return "int32";
+    case WGX_INT8: return "int8";
+    case WGX_UINT8: return "uint8";
+    case WGX_BOOL: return "bool";
+    case WGX_FLOAT64: return "float64";
+    case WGX_INT64: return "int64";
+    default: return "?";
+  }
+}
+
+bool is_float_gemm_dtype(int dt) {
+  return dt == WGX_FLOAT32 || dt == WGX_FLOAT16 || dt == WGX_BFLOAT16;
+}
+
+long long numel(const wgx_tensor* t) {
+  long long n = 1;
+  for (int i = 0; i < t->ndim; ++i) n *= t->shape[i];
+  return n;
+}
+
+}  // namespace
+
+struct wgx_ctx {
+  int device = -1;
+  bool has_dev = false;
+  bool destroyed = false;
+  hipStream_t stream = nullptr;
+  std::string arch = "host";
+  std::map<uintptr_t, Buf> bufs;  // owned buffers by base address
+  std::vector<Cmd> cmds;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool graph_valid = false;
+  int graph_mode = 1;
+  std::string err;
+  std::string last_kernel;
+
+  int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    err = buf;
+    return code;
+  }
+  int hip_fail(hipError_t e, const char* what) {
+    return fail(e == hipErrorOutOfMemory ? WGX_ERR_OOM : WGX_ERR_HIP, "%s: %s", what,
+                hipGetErrorString(e));
+  }
+  void invalidate() {
+    if (exec) hipGraphExecDestroy(exec);
+    if (graph) hipGraphDestroy(graph);
+    exec = nullptr;
+    graph = nullptr;
+    graph_valid = false;
+  }
+  // The owned buffer containing [p, p+bytes), or nullptr.
+  const Buf* find(const void* p, uint64_t bytes, uint64_t* off = nullptr) const {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    auto it = bufs.upper_bound(a);
+    if (it == bufs.begin()) return nullptr;
+    --it;
+    const uint64_t o = a - it->first;
+    if (o > it->second.size || bytes > it->second.size - o) return nullptr;
+    if (off) *off = o;
+    return &it->second;
+  }
+  int check(const wgx_tensor* t, const char* what) {
+    if (!t) return fail(WGX_ERR_INVALID, "%s: tensor is NULL", what);
+    if (elsize(t->dtype) == 0) return fail(WGX_ERR_INVALID, "%s: unknown dtype %d", what, t->dtype);
+    if (t->ndim < 0 || t->ndim > WGX_MAX_NDIM)
+      return fail(WGX_ERR_INVALID, "%s: rank %d exceeds maximum rank of %d", what, t->ndim,
+                  WGX_MAX_NDIM);
+    for (int i = 0; i < t->ndim; ++i)
+      if (t->shape[i] <= 0)
+        return fail(WGX_ERR_INVALID, "%s: dimensions must be positive integers", what);
+    const uint64_t bytes = (uint64_t)numel(t) * elsize(t->dtype);
+    if (!find(t->data, bytes))
+      return fail(WGX_ERR_INVALID, "%s: %llu bytes at %p are not inside a buffer of this context",
+                  what, (unsigned long long)bytes, t->data);
+    return WGX_OK;
+  }
+  hipStream_t dry() const { return has_dev ? describe_only() : name_only(); }
+  int push(std::function<hipError_t(hipStream_t)> fn, const std::string& name) {
+    last_kernel = name;
+    cmds.push_back({std::move(fn), name});
+    invalidate();
+    return WGX_OK;
+  }
+  void* owned_alloc(uint64_t bytes) {
+    void* p = nullptr;
+    if (has_dev) {
+      if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+      if (hipMemset(p, 0, bytes) != hipSuccess) {
+        hipFree(p);
+        return nullptr;
+      }
+    } else {
+      p = aligned_alloc(256, (bytes + 255) / 256 * 256);
+      if (p) memset(p, 0, bytes);
+    }
+    if (p) bufs[reinterpret_cast<uintptr_t>(p)] = {bytes, 0};
+    return p;
+  }
+};
+
+#define CTX_GUARD(c)                                                              \
+  do {                                                                            \
+    if (!(c)) return WGX_ERR_INVALID;                                             \
+    if ((c)->destroyed) return (c)->fail(WGX_ERR_DESTROYED, "WgpuExecutionContext is destroyed"); \
+    if ((c)->has_dev) hipSetDevice((c)->device);                                  \
+  } while (0)
+
+extern "C" {
+
+int wgx_ctx_create(int device, wgx_ctx** out) {
+  if (!out) return WGX_ERR_INVALID;
+  *out = nullptr;
+  wgx_ctx* c = new wgx_ctx();
+  c->device = device;
+  if (device >= 0) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device >= n) {
+      delete c;
+      return WGX_ERR_NO_DEVICE;
+    }
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+      delete c;
+      return WGX_ERR_HIP;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+      std::string a = prop.gcnArchName;
+      c->arch = a.substr(0, a.find(':'));
+    }
+    c->has_dev = true;
+  }
+  *out = c;
+  return WGX_OK;
+}
+
+void wgx_ctx_destroy(wgx_ctx* c) {
+  if (!c) return;
+  if (c->has_dev) {
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+  }
+  c->invalidate();
+  for (auto& kv : c->bufs) {
+    if (c->has_dev)
+      hipFree(reinterpret_cast<void*>(kv.first));
+    else
+      free(reinterpret_cast<void*>(kv.first));
+  }
+  c->bufs.clear();
+  if (c->has_dev && c->stream) hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char* wgx_last_error(const wgx_ctx* c) { return c ? c->err.c_str() : "null context"; }
+int wgx_ctx_has_device(const wgx_ctx* c) { return c && c->has_dev ? 1 : 0; }
+const char* wgx_ctx_arch(const wgx_ctx* c) { return c ? c->arch.c_str() : ""; }
+void* wgx_ctx_stream(const wgx_ctx* c) { return c ? (void*)c->stream : nullptr; }
+const char* wgx_last_kernel(const wgx_ctx* c) { return c ? c->last_kernel.c_str() : ""; }
+int wgx_command_count(const wgx_ctx* c) { return c ? (int)c->cmds.size() : 0; }
+
+int wgx_alloc(wgx_ctx* c, uint64_t bytes, uint32_t usage, void** out) {
+  CTX_GUARD(c);
+  if (!out) return c->fail(WGX_ERR_INVALID, "alloc: out is NULL");
+  const uint64_t sz = bytes < 4 ? 4 : (bytes + 3) / 4 * 4;
+  void* p = c->owned_alloc(sz);
+  if (!p) return c->fail(WGX_ERR_OOM, "alloc: could not allocate %llu bytes", (unsigned long long)sz);
+  c->bufs[reinterpret_cast<uintptr_t>(p)].usage = usage;
+  *out = p;
+  return WGX_OK;
+}
+
+int wgx_buffer_info(const wgx_ctx* c, const void* ptr, uint64_t* base_offset, uint64_t* size,
+                    uint32_t* usage) {
+  if (!c) return WGX_ERR_INVALID;
+  uint64_t off = 0;
+  const Buf* b = c->find(ptr, 0, &off);
+  if (!b) return WGX_ERR_INVALID;
+  if (base_offset) *base_offset = off;
+  if (size) *size = b->size;
+  if (usage) *usage = b->usage;
+  return WGX_OK;
+}
+
+int wgx_write(wgx_ctx* c, void* dst, const void* src, uint64_t bytes) {
+  CTX_GUARD(c);
+  if (bytes == 0) return WGX_OK;
+  if (!c->find(dst, bytes)) return c->fail(WGX_ERR_INVALID, "write: destination range is not an owned buffer");
+  if (!c->has_dev) {
+    memcpy(dst, src, bytes);
+    return WGX_OK;
+  }
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  return e == hipSuccess ? WGX_OK : c->hip_fail(e, "write");
+}
+
+int wgx_read(wgx_ctx* c, const void* src, void* dst, uint64_t bytes) {
+  CTX_GUARD(c);
+  if (bytes == 0) return WGX_OK;
+  if (!c->find(src, bytes)) return c->fail(WGX_ERR_INVALID, "read: source range is not an owned buffer");
+  if (!c->has_dev) {
+    memcpy(dst, src, bytes);
+    return WGX_OK;
+  }
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e == hipSuccess) e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+  return e == hipSuccess ? WGX_OK : c->hip_fail(e, "read");
+}
+
+int wgx_record_copy(wgx_ctx* c, void* dst, const void* src, uint64_t bytes) {
+  CTX_GUARD(c);
+  if (!c->find(src, bytes)) return c->fail(WGX_ERR_INVALID, "copy: source range is not an owned buffer");
+  if (!c->find(dst, bytes)) return c->fail(WGX_ERR_INVALID, "copy: destination range is not an owned buffer");
+  if (bytes == 0 || src == dst) {
+    c->last_kernel = "copy_elided";
+    return WGX_OK;
+  }
+  return c->push([=](hipStream_t s) { return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s); },
+                 "copy_d2d");
+}
+
+// ------------------------------------------------------------------ GEMM family
+
+static int record_gemm(wgx_ctx* c, GemmDesc d) {
+  std::string name;
+  hipError_t e = d.dtype == WGX_FLOAT32 ? launch_gemm_f32(d, c->dry(), &name)
+                                        : launch_gemm_mfma(d, c->dry(), &name);
+  if (e != hipSuccess) return c->hip_fail(e, "kernel set-up");
+  if (d.dtype == WGX_FLOAT32)
+    return c->push([d](hipStream_t s) { return launch_gemm_f32(d, s, nullptr); }, name);
+  return c->push([d](hipStream_t s) { return launch_gemm_mfma(d, s, nullptr); }, name);
+}
+
+int wgx_record_mm(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* bias,
+                  const wgx_tensor* out, float alpha, float beta, uint32_t flags) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(a, "mm: in1")) || (r = c->check(b, "mm: in2")) || (r = c->check(out, "mm: out")))
+    return r;
+  if (bias && (r = c->check(bias, "mm: bias"))) return r;
+  if (!is_float_gemm_dtype(a->dtype) || b->dtype != a->dtype || out->dtype != a->dtype ||
+      (bias && bias->dtype != a->dtype))
+    return c->fail(WGX_ERR_INVALID, "mm: tensors must have matching float32, float16 or bfloat16 dtype");
+  if (a->ndim != 2 || b->ndim != 2 || out->ndim != 2)
+    return c->fail(WGX_ERR_INVALID, "mm: tensors must be 2D matrices");
+  const bool tb = flags & WGX_MM_TRANS_B;
+  const long long M = a->shape[0], K = a->shape[1];
+  const long long K2 = tb ? b->shape[1] : b->shape[0];
+  const long long N = tb ? b->shape[0] : b->shape[1];
+  if (K != K2) return c->fail(WGX_ERR_INVALID, "mm: inner dimensions must match (%lld != %lld)", K, K2);
+  if (out->shape[0] != M || out->shape[1] != N)
+    return c->fail(WGX_ERR_INVALID, "mm: output shape [%lld, %lld] != expected [%lld, %lld]",
+                   (long long)out->shape[0], (long long)out->shape[1], M, N);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || M * K > INT32_MAX || K * N > INT32_MAX || M * N > INT32_MAX)
+    return c->fail(WGX_ERR_INVALID, "mm: matrices above 2^31 elements are not supported");
+  GemmDesc d{};
+  d.dtype = a->dtype;
+  d.batch = 1;
+  d.M = (int)M;
+  d.N = (int)N;
+  d.K = (int)K;
+  d.A = a->data;
+  d.lda = K;
+  d.B = b->data;
+  d.ldb = tb ? K : N;
+  d.bmode = tb ? B_NK : B_KN;
+  d.C = out->data;
+  d.ldc = N;
+  d.alpha = alpha;
+  d.beta = beta;
+  if (bias) {
+    const long long bn = numel(bias);
+    const bool per_col = bn == N && (bias->ndim == 1 || (bias->ndim == 2 && bias->shape[0] == 1));
+    const bool per_row = bn == M && bias->ndim == 2 && bias->shape[1] == 1 && N != 1;
+    if (per_col) d.bias_mode = BIAS_COL;
+    else if (per_row) d.bias_mode = BIAS_ROW;
+    else return c->fail(WGX_ERR_INVALID, "addmm: bias must broadcast as [N], [1,N] or [M,1]");
+    d.bias = bias->data;
+  }
+  return record_gemm(c, d);
+}
+
+int wgx_record_bmm(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* out,
+                   uint32_t flags) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(a, "bmm: a")) || (r = c->check(b, "bmm: b")) || (r = c->check(out, "bmm: out")))
+    return r;
+  if (!is_float_gemm_dtype(a->dtype) || b->dtype != a->dtype || out->dtype != a->dtype)
+    return c->fail(WGX_ERR_INVALID, "bmm: tensors must have matching float32, float16 or bfloat16 dtype");
+  if (a->ndim != 3 || b->ndim != 3 || out->ndim != 3)
+    return c->fail(WGX_ERR_INVALID, "bmm: inputs and output must be 3D");
+  const bool tb = flags & WGX_MM_TRANS_B;
+  const long long B = a->shape[0], M = a->shape[1], K = a->shape[2];
+  const long long K2 = tb ? b->shape[2] : b->shape[1];
+  const long long N = tb ? b->shape[1] : b->shape[2];
+  if (b->shape[0] != B || K2 != K) return c->fail(WGX_ERR_INVALID, "bmm: batch/K mismatch between a and b");
+  if (out->shape[0] != B || out->shape[1] != M || out->shape[2] != N)
+    return c->fail(WGX_ERR_INVALID, "bmm: output shape != [%lld, %lld, %lld]", B, M, N);
+  if (B > 65535) return c->fail(WGX_ERR_INVALID, "bmm: batch above 65535 is not supported");
+  if (M * K > INT32_MAX || K * N > INT32_MAX || M * N > INT32_MAX)
+    return c->fail(WGX_ERR_INVALID, "bmm: matrices above 2^31 elements are not supported");
+  GemmDesc d{};
+  d.dtype = a->dtype;
+  d.batch = (int)B;
+  d.M = (int)M;
+  d.N = (int)N;
+  d.K = (int)K;
+  d.A = a->data;
+  d.lda = K;
+  d.sA = M * K;
+  d.B = b->data;
+  d.ldb = tb ? K : N;
+  d.sB = K * N;
+  d.bmode = tb ? B_NK : B_KN;
+  d.C = out->data;
+  d.ldc = N;
+  d.sC = M * N;
+  d.alpha = 1.0f;
+  d.beta = 1.0f;
+  return record_gemm(c, d);
+}
+
+// ------------------------------------------------------------------ convolution
+
+int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight,
+                      const wgx_tensor* bias, const wgx_conv_args* args, const wgx_tensor* out) {
+  CTX_GUARD(c);
+  int r;
+  if (!args) return c->fail(WGX_ERR_INVALID, "convolution: args is NULL");
+  if ((r = c->check(in, "convolution: input")) || (r = c->check(weight, "convolution: weight")) ||
+      (r = c->check(out, "convolution: output")))
+    return r;
+  if (bias && (r = c->check(bias, "convolution: bias"))) return r;
+  const int dt = in->dtype;
+  if ((dt != WGX_FLOAT32 && dt != WGX_FLOAT16) || weight->dtype != dt || out->dtype != dt)
+    return c->fail(WGX_ERR_INVALID, "convolution: Tensors must have matching float32 or float16 dtype");
+  if (bias && bias->dtype != dt) return c->fail(WGX_ERR_INVALID, "convolution: bias dtype must match input dtype");
+  if (in->ndim != 4 || weight->ndim != 4 || out->ndim != 4)
+    return c->fail(WGX_ERR_INVALID, "convolution: expected 4D tensors for input, weight, and output");
+  const int sH = args->stride[0], sW = args->stride[1], pH = args->padding[0], pW = args->padding[1];
+  const int dH = args->dilation[0], dW = args->dilation[1];
+  const int opH = args->output_padding[0], opW = args->output_padding[1];
+  const int groups = args->groups;
+  if (sH <= 0 || sW <= 0 || dH <= 0 || dW <= 0 || pH < 0 || pW < 0 || groups <= 0)
+    return c->fail(WGX_ERR_INVALID, "convolution: stride, dilation and groups must be positive, padding non-negative");
+  const long long B = in->shape[0], IC = in->shape[1], IH = in->shape[2], IW = in->shape[3];
+  const long long KH = weight->shape[2], KW = weight->shape[3];
+  long long OC;
+  if (IC % groups) return c->fail(WGX_ERR_INVALID, "convolution: IC (%lld) not divisible by groups (%d)", IC, groups);
+  if (args->transposed) {
+    OC = weight->shape[1] * groups;
+    if (weight->shape[0] != IC)
+      return c->fail(WGX_ERR_INVALID, "convolution: weight dim0 !== IC (%lld != %lld)", (long long)weight->shape[0], IC);
+    if (opH >= sH || opW >= sW) return c->fail(WGX_ERR_INVALID, "convolution: output_padding >= stride");
+    if (opH < 0 || opW < 0) return c->fail(WGX_ERR_INVALID, "convolution: negative output_padding");
+    const long long eoh = (IH - 1) * sH - 2LL * pH + (long long)dH * (KH - 1) + opH + 1;
+    const long long eow = (IW - 1) * sW - 2LL * pW + (long long)dW * (KW - 1) + opW + 1;
+    if (out->shape[2] != eoh || out->shape[3] != eow)
+      return c->fail(WGX_ERR_INVALID, "convolution: expected output spatial [%lld, %lld]", eoh, eow);
+  } else {
+    OC = weight->shape[0];
+    if (opH != 0 || opW != 0)
+      return c->fail(WGX_ERR_INVALID, "convolution: non-zero output_padding unsupported for non-transposed conv");
+    if (weight->shape[1] * groups != IC)
+      return c->fail(WGX_ERR_INVALID, "convolution: weight in-ch (%lld) != IC/groups (%lld)",
+                     (long long)weight->shape[1], IC / groups);
+    const long long ohn = IH + 2LL * pH - (long long)dH * (KH - 1) - 1;
+    const long long own = IW + 2LL * pW - (long long)dW * (KW - 1) - 1;
+    if (ohn < 0 || own < 0) return c->fail(WGX_ERR_INVALID, "convolution: invalid geometry (kernel larger than input)");
+    const long long eoh = ohn / sH + 1, eow = own / sW + 1;
+    if (out->shape[2] != eoh || out->shape[3] != eow)
+      return c->fail(WGX_ERR_INVALID, "convolution: expected output spatial [%lld, %lld]", eoh, eow);
+  }
+  if (OC % groups) return c->fail(WGX_ERR_INVALID, "convolution: OC not divisible by groups");
+  if (out->shape[0] != B || out->shape[1] != OC)
+    return c->fail(WGX_ERR_INVALID, "convolution: expected output [%lld, %lld, ...]", B, OC);
+  if (bias && numel(bias) != OC) return c->fail(WGX_ERR_INVALID, "convolution: bias must have OC elements");
+  const long long OH = out->shape[2], OW = out->shape[3];
+  if (B * IC * IH * IW > INT32_MAX || B * OC * OH * OW > INT32_MAX || numel(weight) > INT32_MAX)
+    return c->fail(WGX_ERR_INVALID, "convolution: tensors above 2^31 elements are not supported");
+  const int has_clamp = args->has_clamp ? 1 : 0;
+  const float cmin = args->clamp_min, cmax = args->clamp_max;
+
+  const bool depthwise = !args->transposed && groups == OC && IC == OC && weight->shape[1] == 1;
+  std::string name;
+  hipError_t e;
+  if (depthwise) {
+    DwDesc d{};
+    d.dtype = dt;
+    d.B = (int)B;
+    d.C = (int)IC;
+    d.IH = (int)IH;
+    d.IW = (int)IW;
+    d.OH = (int)OH;
+    d.OW = (int)OW;
+    d.KH = (int)KH;
+    d.KW = (int)KW;
+    d.sH = sH;
+    d.sW = sW;
+    d.pH = pH;
+    d.pW = pW;
+    d.dH = dH;
+    d.dW = dW;
+    d.x = in->data;
+    d.w = weight->data;
+    d.bias = bias ? bias->data : nullptr;
+    d.y = out->data;
+    d.has_clamp = has_clamp;
+    d.cmin = cmin;
+    d.cmax = cmax;
+    e = launch_depthwise(d, c->dry(), &name);
+    if (e == hipSuccess) return c->push([d](hipStream_t s) { return launch_depthwise(d, s, nullptr); }, name);
+    // bands too wide for LDS: fall through to the direct kernel
+  }
+  const bool gemm_ok = !args->transposed && groups == 1 && KH * KW <= 63;
+  if (gemm_ok) {
+    GemmDesc d{};
+    d.dtype = dt;
+    d.batch = (int)B;
+    d.M = (int)OC;
+    d.N = (int)(OH * OW);
+    d.K = (int)(IC * KH * KW);
+    d.A = weight->data;
+    d.lda = d.K;
+    d.sA = 0;
+    d.B = in->data;
+    d.sB = IC * IH * IW;
+    d.C = out->data;
+    d.ldc = OH * OW;
+    d.sC = OC * OH * OW;
+    d.bias = bias ? bias->data : nullptr;
+    d.bias_mode = BIAS_ROW;
+    d.alpha = 1.0f;
+    d.beta = 1.0f;
+    d.has_clamp = has_clamp;
+    d.cmin = cmin;
+    d.cmax = cmax;
+    d.g = ConvGeom{(int)IH, (int)IW, (int)OW, sH, sW, pH, pW, (int)KH, (int)KW, dH, dW};
+    const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0;
+    if (pointwise) {
+      d.bmode = B_KN;  // x[b] is already the [IC, H*W] operand
+      d.ldb = IH * IW;
+    } else {
+      d.bmode = B_CONV;
+      const int rows = conv_ktab_rows(d.K);
+      std::vector<int2> tab(rows);
+      conv_fill_ktab(tab.data(), d.K, (int)IC, d.g);
+      void* dev = c->owned_alloc(sizeof(int2) * rows);
+      if (!dev) return c->fail(WGX_ERR_OOM, "convolution: im2col table allocation failed");
+      if (c->has_dev) {
+        e = hipMemcpy(dev, tab.data(), sizeof(int2) * rows, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return c->hip_fail(e, "convolution: im2col table upload");
+      } else {
+        memcpy(dev, tab.data(), sizeof(int2) * rows);
+      }
+      d.ktab = static_cast<const int2*>(dev);
+    }
+    return record_gemm(c, d);
+  }
+  DirectConvDesc d{};
+  d.dtype = dt;
+  d.transposed = args->transposed ? 1 : 0;
+  d.B = (int)B;
+  d.IC = (int)IC;
+  d.IH = (int)IH;
+  d.IW = (int)IW;
+  d.OC = (int)OC;
+  d.OH = (int)OH;
+  d.OW = (int)OW;
+  d.KH = (int)KH;
+  d.KW = (int)KW;
+  d.sH = sH;
+  d.sW = sW;
+  d.pH = pH;
+  d.pW = pW;
+  d.dH = dH;
+  d.dW = dW;
+  d.groups = groups;
+  d.x = in->data;
+  d.w = weight->data;
+  d.bias = bias ? bias->data : nullptr;
+  d.y = out->data;
+  d.has_clamp = has_clamp;
+  d.cmin = cmin;
+  d.cmax = cmax;
+  e = launch_direct_conv(d, c->dry(), &name);
+  if (e != hipSuccess) return c->hip_fail(e, "kernel set-up");
+  return c->push([d](hipStream_t s) { return launch_direct_conv(d, s, nullptr); }, name);
+}
+
+// ------------------------------------------------------------------ simple ops
+
+static int float_dt(int dt) { return dt == WGX_FLOAT32 || dt == WGX_FLOAT16 || dt == WGX_BFLOAT16; }
+
+static int record_binary(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* out,
+                         float alpha, int op, const char* opname) {
+  int r;
+  if ((r = c->check(a, opname)) || (r = c->check(b, opname)) || (r = c->check(out, opname))) return r;
+  if (!float_dt(a->dtype) || b->dtype != a->dtype || out->dtype != a->dtype)
+    return c->fail(WGX_ERR_INVALID, "%s: tensors must have matching float dtype", opname);
+  if (a->ndim > out->ndim || b->ndim > out->ndim)
+    return c->fail(WGX_ERR_INVALID, "%s: input rank exceeds output rank", opname);
+  BcastDesc d{};
+  d.dtype = a->dtype;
+  d.ndim = out->ndim;
+  d.numel = numel(out);
+  d.a = a->data;
+  d.b = b->data;
+  d.out = out->data;
+  d.alpha = alpha;
+  d.op = op;
+  long long sa = 1, sb = 1;
+  for (int k = out->ndim - 1; k >= 0; --k) {
+    const int ka = k - (out->ndim - a->ndim), kb = k - (out->ndim - b->ndim);
+    const long long da = ka >= 0 ? a->shape[ka] : 1, db = kb >= 0 ? b->shape[kb] : 1;
+    const long long o = out->shape[k];
+    if ((da != o && da != 1) || (db != o && db != 1))
+      return c->fail(WGX_ERR_INVALID, "%s: shapes do not broadcast to the output", opname);
+    d.out_shape[k] = o;
+    d.a_stride[k] = da == 1 ? 0 : sa;
+    d.b_stride[k] = db == 1 ? 0 : sb;
+    sa *= da;
+    sb *= db;
+  }
+  std::string name;
+  launch_binary(d, c->dry(), &name);
+  return c->push([d](hipStream_t s) { return launch_binary(d, s, nullptr); }, name);
+}
+
+int wgx_record_add(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, float alpha, int subtract,
+                   const wgx_tensor* out) {
+  CTX_GUARD(c);
+  return record_binary(c, a, b, out, subtract ? -alpha : alpha, 0, subtract ? "sub" : "add");
+}
+
+int wgx_record_mul(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* out) {
+  CTX_GUARD(c);
+  return record_binary(c, a, b, out, 1.0f, 1, "mul");
+}
+
+int wgx_record_unary(wgx_ctx* c, int op, const wgx_tensor* in, const wgx_tensor* out) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(in, "unary: in")) || (r = c->check(out, "unary: out"))) return r;
+  if (op < 0 || op > 3) return c->fail(WGX_ERR_INVALID, "unary: unknown op %d", op);
+  if (!float_dt(in->dtype) || out->dtype != in->dtype || numel(in) != numel(out))
+    return c->fail(WGX_ERR_INVALID, "unary: input and output must have the same float dtype and size");
+  const int dt = in->dtype;
+  const long long n = numel(in);
+  const void* x = in->data;
+  void* y = out->data;
+  std::string name;
+  launch_unary(op, dt, n, x, y, c->dry(), &name);
+  return c->push([=](hipStream_t s) { return launch_unary(op, dt, n, x, y, s, nullptr); }, name);
+}
+
+static int norm_dim(int dim, int ndim) { return dim < 0 ? dim + ndim : dim; }
+
+int wgx_record_cat(wgx_ctx* c, const wgx_tensor* inputs, int n_inputs, int dim, const wgx_tensor* out) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(out, "cat: out"))) return r;
+  if (n_inputs <= 0 || !inputs) return c->fail(WGX_ERR_INVALID, "cat: no inputs");
+  const int d = norm_dim(dim, out->ndim);
+  if (d < 0 || d >= out->ndim) return c->fail(WGX_ERR_INVALID, "cat: dim out of range");
+  long long total = 0;
+  for (int i = 0; i < n_inputs; ++i) {
+    const wgx_tensor* t = &inputs[i];
+    if ((r = c->check(t, "cat: input"))) return r;
+    if (t->dtype != out->dtype || t->ndim != out->ndim)
+      return c->fail(WGX_ERR_INVALID, "cat: inputs must match the output dtype and rank");
+    for (int k = 0; k < out->ndim; ++k)
+      if (k != d && t->shape[k] != out->shape[k])
+        return c->fail(WGX_ERR_INVALID, "cat: input %d shape mismatch at dim %d", i, k);
+    total += t->shape[d];
+  }
+  if (total != out->shape[d]) return c->fail(WGX_ERR_INVALID, "cat: sizes along dim do not add up");
+  long long outer = 1, inner = 1;
+  for (int k = 0; k < d; ++k) outer *= out->shape[k];
+  for (int k = d + 1; k < out->ndim; ++k) inner *= out->shape[k];
+  const int es = elsize(out->dtype);
+  long long off = 0;
+  for (int i = 0; i < n_inputs; ++i) {
+    const long long is = inputs[i].shape[d] * inner, os = out->shape[d] * inner, doff = off * inner;
+    const void* src = inputs[i].data;
+    void* dst = out->data;
+    std::string name;
+    launch_slab_copy(es, outer, is, os, doff, 0, src, dst, false, c->dry(), &name);
+    c->push([=](hipStream_t s) { return launch_slab_copy(es, outer, is, os, doff, 0, src, dst, false, s, nullptr); },
+            name);
+    off += inputs[i].shape[d];
+  }
+  return WGX_OK;
+}
+
+int wgx_record_split(wgx_ctx* c, const wgx_tensor* in, int dim, const wgx_tensor* outputs, int n_outputs) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(in, "split: in"))) return r;
+  if (n_outputs <= 0 || !outputs) return c->fail(WGX_ERR_INVALID, "split: no outputs");
+  const int d = norm_dim(dim, in->ndim);
+  if (d < 0 || d >= in->ndim) return c->fail(WGX_ERR_INVALID, "split: dim out of range");
+  long long total = 0;
+  for (int i = 0; i < n_outputs; ++i) {
+    const wgx_tensor* t = &outputs[i];
+    if ((r = c->check(t, "split: output"))) return r;
+    if (t->dtype != in->dtype || t->ndim != in->ndim)
+      return c->fail(WGX_ERR_INVALID, "split: outputs must match the input dtype and rank");
+    for (int k = 0; k < in->ndim; ++k)
+      if (k != d && t->shape[k] != in->shape[k])
+        return c->fail(WGX_ERR_INVALID, "split: output %d shape mismatch at dim %d", i, k);
+    total += t->shape[d];
+  }
+  if (total != in->shape[d]) return c->fail(WGX_ERR_INVALID, "split: sizes along dim do not add up");
+  long long outer = 1, inner = 1;
+  for (int k = 0; k < d; ++k) outer *= in->shape[k];
+  for (int k = d + 1; k < in->ndim; ++k) inner *= in->shape[k];
+  const int es = elsize(in->dtype);
+  long long off = 0;
+  for (int i = 0; i < n_outputs; ++i) {
+    const long long is = in->shape[d] * inner, os = outputs[i].shape[d] * inner, soff = off * inner;
+    const void* src = in->data;
+    void* dst = outputs[i].data;
+    std::string name;
+    launch_slab_copy(es, outer, is, os, 0, soff, src, dst, true, c->dry(), &name);
+    c->push([=](hipStream_t s) { return launch_slab_copy(es, outer, is, os, 0, soff, src, dst, true, s, nullptr); },
+            name);
+    off += outputs[i].shape[d];
+  }
+  return WGX_OK;
+}
+
+int wgx_record_upsample_nearest2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* out) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(in, "upsample: in")) || (r = c->check(out, "upsample: out"))) return r;
+  if (!float_dt(in->dtype) || out->dtype != in->dtype || in->ndim != 4 || out->ndim != 4 ||
+      in->shape[0] != out->shape[0] || in->shape[1] != out->shape[1])
+    return c->fail(WGX_ERR_INVALID, "upsample: expected 4D float tensors with matching N, C");
+  const int dt = in->dtype;
+  const int BC = (int)(in->shape[0] * in->shape[1]);
+  const int IH = (int)in->shape[2], IW = (int)in->shape[3], OH = (int)out->shape[2], OW = (int)out->shape[3];
+  const void* x = in->data;
+  void* y = out->data;
+  std::string name;
+  launch_upsample_nearest(dt, BC, IH, IW, OH, OW, x, y, c->dry(), &name);
+  return c->push([=](hipStream_t s) { return launch_upsample_nearest(dt, BC, IH, IW, OH, OW, x, y, s, nullptr); },
+                 name);
+}
+
+int wgx_record_max_pool2d(wgx_ctx* c, const wgx_tensor* in, const int32_t kernel[2], const int32_t stride[2],
+                          const int32_t padding[2], const int32_t dilation[2], const wgx_tensor* out) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(in, "max_pool2d: in")) || (r = c->check(out, "max_pool2d: out"))) return r;
+  if (!float_dt(in->dtype) || out->dtype != in->dtype || in->ndim != 4 || out->ndim != 4)
+    return c->fail(WGX_ERR_INVALID, "max_pool2d: expected 4D float tensors");
+  const int KH = kernel[0], KW = kernel[1], sH = stride[0], sW = stride[1], pH = padding[0], pW = padding[1];
+  const int dH = dilation[0], dW = dilation[1];
+  if (KH <= 0 || KW <= 0 || sH <= 0 || sW <= 0 || dH <= 0 || dW <= 0 || pH < 0 || pW < 0)
+    return c->fail(WGX_ERR_INVALID, "max_pool2d: invalid kernel/stride/padding/dilation");
+  const long long IH = in->shape[2], IW = in->shape[3];
+  const long long eoh = (IH + 2LL * pH - (long long)dH * (KH - 1) - 1) / sH + 1;
+  const long long eow = (IW + 2LL * pW - (long long)dW * (KW - 1) - 1) / sW + 1;
+  if (out->shape[0] != in->shape[0] || out->shape[1] != in->shape[1] || out->shape[2] != eoh || out->shape[3] != eow)
+    return c->fail(WGX_ERR_INVALID, "max_pool2d: expected output spatial [%lld, %lld]", eoh, eow);
+  const int dt = in->dtype;
+  const int BC = (int)(in->shape[0] * in->shape[1]);
+  const void* x = in->data;
+  void* y = out->data;
+  const int ih = (int)IH, iw = (int)IW, oh = (int)eoh, ow = (int)eow;
+  std::string name;
+  launch_max_pool(dt, BC, ih, iw, oh, ow, KH, KW, sH, sW, pH, pW, dH, dW, x, y, c->dry(), &name);
+  return c->push([=](hipStream_t s) {
+    return launch_max_pool(dt, BC, ih, iw, oh, ow, KH, KW, sH, sW, pH, pW, dH, dW, x, y, s, nullptr);
+  }, name);
+}
+
+// ------------------------------------------------------------------ execution
+
+static int run_eager(wgx_ctx* c) {
+  for (const Cmd& cmd : c->cmds) {
+    hipError_t e = cmd.fn(c->stream);
+    if (e != hipSuccess) return c->hip_fail(e, cmd.name.c_str());
+  }
+  return WGX_OK;
+}
+
+int wgx_submit(wgx_ctx* c) {
+  CTX_GUARD(c);
+  if (c->cmds.empty()) return WGX_OK;
+  if (!c->has_dev) return c->fail(WGX_ERR_NO_DEVICE, "submit: host-only context has no device");
+  if (!c->graph_mode) return run_eager(c);
+  if (!c->graph_valid) {
+    hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return c->hip_fail(e, "submit: begin capture");
+    int r = WGX_OK;
+    for (const Cmd& cmd : c->cmds) {
+      e = cmd.fn(c->stream);
+      if (e != hipSuccess) {
+        r = c->hip_fail(e, cmd.name.c_str());
+        break;
+      }
+    }
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(c->stream, &g);
+    if (r != WGX_OK) {
+      if (g) hipGraphDestroy(g);
+      return r;
+    }
+    if (e2 != hipSuccess) return c->hip_fail(e2, "submit: end capture");
+    c->graph = g;
+    e = hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+      c->invalidate();
+      return c->hip_fail(e, "submit: graph instantiate");
+    }
+    c->graph_valid = true;
+  }
+  hipError_t e = hipGraphLaunch(c->exec, c->stream);
+  return e == hipSuccess ? WGX_OK : c->hip_fail(e, "submit: graph launch");
+}
+
+int wgx_sync(wgx_ctx* c) {
+  CTX_GUARD(c);
+  if (!c->has_dev) return WGX_OK;
+  hipError_t e = hipStreamSynchronize(c->stream);
+  return e == hipSuccess ? WGX_OK : c->hip_fail(e, "sync");
+}
+
+int wgx_reset(wgx_ctx* c) {
+  CTX_GUARD(c);
+  c->cmds.clear();
+  c->invalidate();
+  return WGX_OK;
+}
+
+int wgx_set_graph_mode(wgx_ctx* c, int enabled) {
+  CTX_GUARD(c);
+  c->graph_mode = enabled ? 1 : 0;
+  c->invalidate();
+  return WGX_OK;
+}
+
+int wgx_time_submits(wgx_ctx* c, int reps, float* ms_per_submit) {
+  CTX_GUARD(c);
+  if (!c->has_dev) return c->fail(WGX_ERR_NO_DEVICE, "time: host-only context has no device");
+  if (reps <= 0 || !ms_per_submit) return c->fail(WGX_ERR_INVALID, "time: reps must be positive");
+  hipEvent_t a, b;
+  hipError_t e = hipEventCreate(&a);
+  if (e != hipSuccess) return c->hip_fail(e, "time: event");
+  e = hipEventCreate(&b);
+  if (e != hipSuccess) {
+    hipEventDestroy(a);
+    return c->hip_fail(e, "time: event");
+  }
+  int r = WGX_OK;
+  e = hipEventRecord(a, c->stream);
+  for (int i = 0; i < reps && e == hipSuccess && r == WGX_OK; ++i) r = wgx_submit(c);
+  if (e == hipSuccess && r == WGX_OK) e = hipEventRecord(b, c->stream);
+  if (e == hipSuccess && r == WGX_OK) e = hipEventSynchronize(b);
+  float ms = 0.f;
+  if (e == hipSuccess && r == WGX_OK) e = hipEventElapsedTime(&ms, a, b);
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  if (r != WGX_OK) return r;
+  if (e != hipSuccess) return c->hip_fail(e, "time");
+  *ms_per_submit = ms / reps;
+  return WGX_OK;
+}
+
+}  // extern "C"
