@@ -37,7 +37,7 @@ PEAK = {  # MI355X published dense peaks
     "fp32_TFLOPs": 157.3,
 }
 CONV2 = {
-    "2a": dict(x=(1, 64, 80, 80), w=(128, 64, 3, 3), s=(2 - 1, 1), p=(1, 1), y=(1, 128, 80, 80)),
+    "2a": dict(x=(1, 64, 80, 80), w=(128, 64, 3, 3), s=(1, 1), p=(1, 1), y=(1, 128, 80, 80)),
     "2b": dict(x=(1, 128, 80, 80), w=(256, 128, 3, 3), s=(2, 2), p=(1, 1), y=(1, 256, 40, 40)),
 }
 

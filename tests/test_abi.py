@@ -83,7 +83,7 @@ def test_mm_validation(hctx, pkg):
         hctx.mm(hctx.tensor("float16", [4, 8]), b, o)
     h = [hctx.tensor("float16", s) for s in ([64, 96], [96, 80], [64, 80])]
     hctx.mm(*h)
-    assert hctx.last_kernel.startswith("gemm_mfma_f16") and hctx.last_kernel.endswith("kn")
+    assert hctx.last_kernel.startswith("gemm_mfma_f16") and "_kn" in hctx.last_kernel
     hctx.mm(h[0], hctx.tensor("float16", [80, 96]), h[2], trans_b=True)
     assert hctx.last_kernel.endswith("nk")
     with pytest.raises(E, match="bias"):
@@ -115,7 +115,7 @@ def test_conv_validation_and_variants(hctx, pkg):
 
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)).endswith("_conv")
     assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)).endswith("_conv")
-    assert conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8]).endswith("_kn")
+    assert "_kn" in conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8])
     assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3"
     assert conv([1, 512, 20, 20], [512, 1, 5, 5], [1, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5"
     assert conv([1, 8, 10, 10], [12, 4, 3, 3], [1, 12, 10, 10], pad=(1, 1), groups=2) == "conv_grouped_direct"

@@ -30,7 +30,7 @@ struct KParams {
   const float* B;
   float* C;
   const float* bias;
-  const int2* ktab;
+  const uint32_t* ktab;
   int M, N, K;
   long long lda, ldb, ldc, sA, sB, sC;
   int bias_mode;
@@ -47,6 +47,7 @@ __global__ __launch_bounds__(NT) void k_sgemm(KParams p) {
   constexpr int PA = BM + 4, PB = BN + 4;
   __shared__ float sA[2][BK][PA];
   __shared__ float sB[2][BK][PB];
+  extern __shared__ uint32_t ktab_lds[];  // B_CONV: the per-k table, (offset << 6) | tap
   constexpr int TX = BN / TN;
   constexpr int ACH = BM * BK / 4;  // 4-float A chunks per tile
   constexpr int BCH = BN * BK / 4;  // 4-float B chunks per tile
@@ -89,6 +90,8 @@ __global__ __launch_bounds__(NT) void k_sgemm(KParams p) {
   float rc[BMODE == B_CONV ? KRc : 1];
 
   // rows of 4 consecutive k (A, and B in the B_NK form)
+  // Loads are unconditional from clamped in-bounds addresses, zeroed after
+  // with a select, so a tile's loads are all in flight together.
   auto load_krows = [&](const float* __restrict__ src, long long ld, int r0, int rlim, int k0,
                         bool vec, float4* dst, int nch, int total) {
 #pragma unroll
@@ -98,16 +101,20 @@ __global__ __launch_bounds__(NT) void k_sgemm(KParams p) {
       if (c < total) {
         const int row = c / (BK / 4), kq = c % (BK / 4);
         const int gr = r0 + row, gk = k0 + kq * 4;
-        if (gr < rlim) {
-          const float* s = src + gr * ld + gk;
-          if (vec) {
-            if (gk < K) v = *reinterpret_cast<const float4*>(s);
-          } else {
-            if (gk < K) v.x = s[0];
-            if (gk + 1 < K) v.y = s[1];
-            if (gk + 2 < K) v.z = s[2];
-            if (gk + 3 < K) v.w = s[3];
+        const float* s = src + (long long)(gr < rlim ? gr : rlim - 1) * ld;
+        if (vec) {
+          const bool ok = gr < rlim && gk < K;
+          const float4 t = *reinterpret_cast<const float4*>(s + (ok ? gk : 0));
+          v = ok ? t : v;
+        } else {
+          float t[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = gr < rlim && gk + e < K;
+            const float x = s[ok ? gk + e : 0];
+            t[e] = ok ? x : 0.f;
           }
+          v = make_float4(t[0], t[1], t[2], t[3]);
         }
       }
       dst[i] = v;
@@ -126,31 +133,37 @@ __global__ __launch_bounds__(NT) void k_sgemm(KParams p) {
         if (c < BCH) {
           const int kr = c / (BN / 4), nq = c % (BN / 4);
           const int gk = k0 + kr, gn = n0 + nq * 4;
-          if (gk < K) {
-            const float* s = Bp + (long long)gk * p.ldb + gn;
-            if (BVEC) {
-              if (gn < N) v = *reinterpret_cast<const float4*>(s);
-            } else {
-              if (gn < N) v.x = s[0];
-              if (gn + 1 < N) v.y = s[1];
-              if (gn + 2 < N) v.z = s[2];
-              if (gn + 3 < N) v.w = s[3];
+          const float* s = Bp + (long long)(gk < K ? gk : K - 1) * p.ldb;
+          if (BVEC) {
+            const bool ok = gk < K && gn < N;
+            const float4 t = *reinterpret_cast<const float4*>(s + (ok ? gn : 0));
+            v = ok ? t : v;
+          } else {
+            float t[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const bool ok = gk < K && gn + e < N;
+              const float x = s[ok ? gn + e : 0];
+              t[e] = ok ? x : 0.f;
             }
+            v = make_float4(t[0], t[1], t[2], t[3]);
           }
         }
         rb[i] = v;
       }
     } else {
       const int kb = k0 + krun * KRc;
+      uint32_t ent[KRc];
+#pragma unroll
+      for (int e = 0; e < KRc; ++e) ent[e] = ktab_lds[kb + e];
+      float t[KRc];
 #pragma unroll
       for (int e = 0; e < KRc; ++e) {
-        float v = 0.f;
-        if (krun * KRc < BK) {
-          const int2 t = p.ktab[kb + e];
-          if ((cmask >> t.y) & 1ull) v = Bp[colbase + t.x];
-        }
-        rc[e] = v;
+        const bool ok = (cmask >> (ent[e] & 63u)) & 1ull;
+        t[e] = Bp[ok ? colbase + (int)(ent[e] >> 6) : 0];
       }
+#pragma unroll
+      for (int e = 0; e < KRc; ++e) rc[e] = ((cmask >> (ent[e] & 63u)) & 1ull) ? t[e] : 0.f;
     }
   };
 
@@ -202,6 +215,11 @@ __global__ __launch_bounds__(NT) void k_sgemm(KParams p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = 0.f;
 
   const int KT = (K + BK - 1) / BK;
+  if constexpr (BMODE == B_CONV) {
+    const int rows = (K + 63) / 64 * 64;
+    for (int i = tid; i < rows; i += NT) ktab_lds[i] = p.ktab[i];
+    __syncthreads();
+  }
   load_tile(0);
   store_tile(0);
   __syncthreads();
@@ -253,10 +271,11 @@ __global__ __launch_bounds__(NT) void k_sgemm(KParams p) {
 
 template <int BM, int BN, int TM, int TN, int BMODE, bool AVEC, bool BVEC>
 hipError_t launch_one(const KParams& kp, int batch, hipStream_t s) {
+  const size_t lds = BMODE == B_CONV ? (size_t)conv_ktab_rows(kp.K) * sizeof(uint32_t) : 0;
   if (is_dry(s)) return hipSuccess;
   const int tiles_m = (kp.M + BM - 1) / BM;
   dim3 grid(tiles_m * kp.tiles_n, 1, batch);
-  hipLaunchKernelGGL((k_sgemm<BM, BN, TM, TN, BMODE, AVEC, BVEC>), grid, dim3(NT), 0, s, kp);
+  hipLaunchKernelGGL((k_sgemm<BM, BN, TM, TN, BMODE, AVEC, BVEC>), grid, dim3(NT), lds, s, kp);
   return hipGetLastError();
 }
 

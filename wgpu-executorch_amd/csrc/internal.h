@@ -50,14 +50,16 @@ struct GemmDesc {
   float cmin, cmax;
   int bmode;
   ConvGeom g;
-  const int2* ktab;  // device table for B_CONV, Kpad entries {off, tap}
+  const uint32_t* ktab;  // device table for B_CONV: Kpad entries (off << 6) | tap
 };
 
 // Table rows needed for a B_CONV launch (K rounded up to the largest K tile).
 int conv_ktab_rows(int K);
-// Fills a host table for B_CONV: entry k = {ic*IH*IW + kh*dH*IW + kw*dW, kh*KW+kw};
+// Fills a host table for B_CONV: entry k = (ic*IH*IW + kh*dH*IW + kw*dW) << 6 | (kh*KW+kw);
 // padding entries get tap 63 (never inside the image).
-void conv_fill_ktab(int2* tab, int K, int IC, const ConvGeom& g);
+void conv_fill_ktab(uint32_t* tab, int K, int IC, const ConvGeom& g);
+// The packed table applies: KH*KW <= 63, offsets < 2^26, table <= 32 KB.
+bool conv_ktab_fits(int K, int IC, const ConvGeom& g);
 
 hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name);
 hipError_t launch_gemm_f32(const GemmDesc& d, hipStream_t s, std::string* name);

@@ -490,7 +490,10 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
     if (e == hipSuccess) return c->push([d](hipStream_t s) { return launch_depthwise(d, s, nullptr); }, name);
     // bands too wide for LDS: fall through to the direct kernel
   }
-  const bool gemm_ok = !args->transposed && groups == 1 && KH * KW <= 63;
+  const ConvGeom geom{(int)IH, (int)IW, (int)OW, sH, sW, pH, pW, (int)KH, (int)KW, dH, dW};
+  const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0;
+  const bool gemm_ok = !args->transposed && groups == 1 &&
+                       (pointwise || conv_ktab_fits((int)(IC * KH * KW), (int)IC, geom));
   if (gemm_ok) {
     GemmDesc d{};
     d.dtype = dt;
@@ -513,25 +516,24 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
     d.has_clamp = has_clamp;
     d.cmin = cmin;
     d.cmax = cmax;
-    d.g = ConvGeom{(int)IH, (int)IW, (int)OW, sH, sW, pH, pW, (int)KH, (int)KW, dH, dW};
-    const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0;
+    d.g = geom;
     if (pointwise) {
       d.bmode = B_KN;  // x[b] is already the [IC, H*W] operand
       d.ldb = IH * IW;
     } else {
       d.bmode = B_CONV;
       const int rows = conv_ktab_rows(d.K);
-      std::vector<int2> tab(rows);
+      std::vector<uint32_t> tab(rows);
       conv_fill_ktab(tab.data(), d.K, (int)IC, d.g);
-      void* dev = c->owned_alloc(sizeof(int2) * rows);
+      void* dev = c->owned_alloc(sizeof(uint32_t) * rows);
       if (!dev) return c->fail(WGX_ERR_OOM, "convolution: im2col table allocation failed");
       if (c->has_dev) {
-        e = hipMemcpy(dev, tab.data(), sizeof(int2) * rows, hipMemcpyHostToDevice);
+        e = hipMemcpy(dev, tab.data(), sizeof(uint32_t) * rows, hipMemcpyHostToDevice);
         if (e != hipSuccess) return c->hip_fail(e, "convolution: im2col table upload");
       } else {
-        memcpy(dev, tab.data(), sizeof(int2) * rows);
+        memcpy(dev, tab.data(), sizeof(uint32_t) * rows);
       }
-      d.ktab = static_cast<const int2*>(dev);
+      d.ktab = static_cast<const uint32_t*>(dev);
     }
     return record_gemm(c, d);
   }
