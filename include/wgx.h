@@ -10,7 +10,8 @@
  * message of the last failure is available from wgx_last_error().
  *
  * Model (mirrors the reference's record/submit split, src/context.ts:17-390):
- *   - a context owns one HIP stream and every buffer it allocated;
+ *   - a context owns every buffer it allocated; all contexts of one device
+ *     share that device's single HIP stream (GPUDevice.queue);
  *   - wgx_record_* validate and append a launch record, nothing runs yet;
  *   - wgx_submit replays the recorded list in order (as one HIP graph,
  *     re-captured only when the list changed), wgx_sync waits for it;
@@ -94,8 +95,14 @@ typedef struct wgx_ctx wgx_ctx;
 /* new WgpuExecutionContext(device) (src/context.ts:28-30).  device >= 0 is a
  * HIP device ordinal; -1 makes a host-only validation context. */
 int wgx_ctx_create(int device, wgx_ctx** out);
-/* destroy() (src/context.ts:61-72): frees every owned buffer; idempotent on
- * the handle's contents, the handle itself is freed. */
+/* A further context on the same device as `parent`: it shares the parent's
+ * buffer registry and queue (one HIP stream per device, so work submitted
+ * from any context runs in submission order, like GPUDevice.queue) and has
+ * its own command list.  This is how several WgpuExecutionContexts are
+ * created over one GPUDevice (src/context.ts:28-30). */
+int wgx_ctx_create_shared(wgx_ctx* parent, wgx_ctx** out);
+/* destroy() (src/context.ts:61-72): frees every buffer this context
+ * allocated and the handle; the device state goes with the last context. */
 void wgx_ctx_destroy(wgx_ctx* ctx);
 /* Message of the most recent failure on this context ("" if none). */
 const char* wgx_last_error(const wgx_ctx* ctx);
@@ -111,6 +118,10 @@ void* wgx_ctx_stream(const wgx_ctx* ctx);
 /* storageBuffer(size) (src/context.ts:86-92): a context-owned buffer of at
  * least max(4, round_up(bytes, 4)) bytes, 256-byte aligned, zero-filled. */
 int wgx_alloc(wgx_ctx* ctx, uint64_t bytes, uint32_t usage, void** out);
+/* GPUBuffer.destroy(): frees the buffer whose base address is ptr (any
+ * context of the device may free it).  A later submit of a command recorded
+ * against it fails with WGX_ERR_INVALID instead of touching freed memory. */
+int wgx_free(wgx_ctx* ctx, void* ptr);
 /* Size and usage of the owned buffer that contains ptr (0 / error if none). */
 int wgx_buffer_info(const wgx_ctx* ctx, const void* ptr, uint64_t* base_offset,
                     uint64_t* size, uint32_t* usage);

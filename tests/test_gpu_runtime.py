@@ -115,3 +115,32 @@ def test_elementwise_ops(pkg, orc):
         np.testing.assert_array_equal(mp.get_f32(), ref)
     finally:
         ctx.destroy()
+
+
+def test_shared_contexts_order_and_freed_buffers(pkg):
+    """Two contexts over one device share its queue: work submitted from one
+    is visible to the other's later submit without a sync in between.  A
+    command whose buffer was freed fails at submit instead of touching it."""
+    W = pkg.wgx
+    a = W.Context(0)
+    b = a.shared()
+    try:
+        x = a.tensor("float32", [1024]).set_data(np.arange(1024, dtype=np.float32))
+        y = a.tensor("float32", [1024])
+        z = b.tensor("float32", [1024])
+        a.copy(x, y)
+        b.copy(y, z)
+        a.submit()
+        b.submit()
+        b.sync()
+        assert np.array_equal(z.get_data(), np.arange(1024, dtype=np.float32))
+        p = a.storage_buffer(64)
+        t = a.tensor("float32", [16], buffer=p)
+        b.reset()
+        b.copy(t, z)
+        a.free(p)
+        with pytest.raises(W.WgxError, match="destroyed buffer"):
+            b.submit()
+    finally:
+        b.destroy()
+        a.destroy()

@@ -36,11 +36,29 @@ namespace {
 struct Buf {
   uint64_t size;
   uint32_t usage;
+  uint64_t serial;      // allocation number, so a recycled address is not mistaken for it
+  const void* owner;    // the context that allocated it (freed with that context)
 };
+
+// (buffer base, allocation serial) pairs a command reads or writes
+using Uses = std::vector<std::pair<uintptr_t, uint64_t>>;
 
 struct Cmd {
   std::function<hipError_t(hipStream_t)> fn;
   std::string name;
+  Uses uses;
+};
+
+// What every context on one device shares: the buffer registry and the queue
+// (a single HIP stream), like a GPUDevice and its queue.
+struct DeviceState {
+  int device = -1;
+  bool has_dev = false;
+  hipStream_t stream = nullptr;
+  std::string arch = "host";
+  std::map<uintptr_t, Buf> bufs;
+  uint64_t next_serial = 1;
+  int refs = 0;
 };
 
 int elsize(int dt) {
@@ -91,12 +109,9 @@ long long numel(const wgx_tensor* t) {
 }  // namespace
 
 struct wgx_ctx {
-  int device = -1;
-  bool has_dev = false;
+  DeviceState* d = nullptr;
   bool destroyed = false;
-  hipStream_t stream = nullptr;
-  std::string arch = "host";
-  std::map<uintptr_t, Buf> bufs;  // owned buffers by base address
+  Uses cur_uses;  // buffers named by the record call in progress
   std::vector<Cmd> cmds;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -126,15 +141,24 @@ struct wgx_ctx {
     graph_valid = false;
   }
   // The owned buffer containing [p, p+bytes), or nullptr.
-  const Buf* find(const void* p, uint64_t bytes, uint64_t* off = nullptr) const {
+  const Buf* find(const void* p, uint64_t bytes, uint64_t* off = nullptr,
+                  uintptr_t* base = nullptr) const {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    auto it = bufs.upper_bound(a);
-    if (it == bufs.begin()) return nullptr;
+    auto it = d->bufs.upper_bound(a);
+    if (it == d->bufs.begin()) return nullptr;
     --it;
     const uint64_t o = a - it->first;
     if (o > it->second.size || bytes > it->second.size - o) return nullptr;
     if (off) *off = o;
+    if (base) *base = it->first;
     return &it->second;
+  }
+  // find() that also notes the buffer as used by the record in progress
+  const Buf* use(const void* p, uint64_t bytes) {
+    uintptr_t base = 0;
+    const Buf* b = find(p, bytes, nullptr, &base);
+    if (b) cur_uses.emplace_back(base, b->serial);
+    return b;
   }
   int check(const wgx_tensor* t, const char* what) {
     if (!t) return fail(WGX_ERR_INVALID, "%s: tensor is NULL", what);
@@ -146,21 +170,32 @@ struct wgx_ctx {
       if (t->shape[i] <= 0)
         return fail(WGX_ERR_INVALID, "%s: dimensions must be positive integers", what);
     const uint64_t bytes = (uint64_t)numel(t) * elsize(t->dtype);
-    if (!find(t->data, bytes))
+    if (!use(t->data, bytes))
       return fail(WGX_ERR_INVALID, "%s: %llu bytes at %p are not inside a buffer of this context",
                   what, (unsigned long long)bytes, t->data);
     return WGX_OK;
   }
-  hipStream_t dry() const { return has_dev ? describe_only() : name_only(); }
+  hipStream_t dry() const { return d->has_dev ? describe_only() : name_only(); }
   int push(std::function<hipError_t(hipStream_t)> fn, const std::string& name) {
     last_kernel = name;
-    cmds.push_back({std::move(fn), name});
+    cmds.push_back({std::move(fn), name, cur_uses});
     invalidate();
+    return WGX_OK;
+  }
+  // Every buffer the recorded commands use must still be the allocation they
+  // were recorded against.
+  int check_uses() {
+    for (const Cmd& cmd : cmds)
+      for (const auto& u : cmd.uses) {
+        auto it = d->bufs.find(u.first);
+        if (it == d->bufs.end() || it->second.serial != u.second)
+          return fail(WGX_ERR_INVALID, "submit: '%s' uses a destroyed buffer", cmd.name.c_str());
+      }
     return WGX_OK;
   }
   void* owned_alloc(uint64_t bytes) {
     void* p = nullptr;
-    if (has_dev) {
+    if (d->has_dev) {
       if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
       if (hipMemset(p, 0, bytes) != hipSuccess) {
         hipFree(p);
@@ -170,8 +205,15 @@ struct wgx_ctx {
       p = aligned_alloc(256, (bytes + 255) / 256 * 256);
       if (p) memset(p, 0, bytes);
     }
-    if (p) bufs[reinterpret_cast<uintptr_t>(p)] = {bytes, 0};
+    if (p) d->bufs[reinterpret_cast<uintptr_t>(p)] = {bytes, 0, d->next_serial++, this};
     return p;
+  }
+  void release(uintptr_t base) {
+    if (d->has_dev)
+      hipFree(reinterpret_cast<void*>(base));
+    else
+      free(reinterpret_cast<void*>(base));
+    d->bufs.erase(base);
   }
 };
 
@@ -179,7 +221,8 @@ struct wgx_ctx {
   do {                                                                            \
     if (!(c)) return WGX_ERR_INVALID;                                             \
     if ((c)->destroyed) return (c)->fail(WGX_ERR_DESTROYED, "WgpuExecutionContext is destroyed"); \
-    if ((c)->has_dev) hipSetDevice((c)->device);                                  \
+    if ((c)->d->has_dev) hipSetDevice((c)->d->device);                            \
+    (c)->cur_uses.clear();                                                        \
   } while (0)
 
 extern "C" {
@@ -187,51 +230,82 @@ extern "C" {
 int wgx_ctx_create(int device, wgx_ctx** out) {
   if (!out) return WGX_ERR_INVALID;
   *out = nullptr;
-  wgx_ctx* c = new wgx_ctx();
-  c->device = device;
+  DeviceState* ds = new DeviceState();
+  ds->device = device;
   if (device >= 0) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || device >= n) {
-      delete c;
+      delete ds;
       return WGX_ERR_NO_DEVICE;
     }
-    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
-      delete c;
+    if (hipSetDevice(device) != hipSuccess ||
+        hipStreamCreateWithFlags(&ds->stream, hipStreamNonBlocking) != hipSuccess) {
+      delete ds;
       return WGX_ERR_HIP;
     }
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
       std::string a = prop.gcnArchName;
-      c->arch = a.substr(0, a.find(':'));
+      ds->arch = a.substr(0, a.find(':'));
     }
-    c->has_dev = true;
+    ds->has_dev = true;
   }
+  wgx_ctx* c = new wgx_ctx();
+  c->d = ds;
+  ds->refs = 1;
+  *out = c;
+  return WGX_OK;
+}
+
+int wgx_ctx_create_shared(wgx_ctx* parent, wgx_ctx** out) {
+  if (!parent || !out) return WGX_ERR_INVALID;
+  *out = nullptr;
+  if (parent->destroyed) return parent->fail(WGX_ERR_DESTROYED, "WgpuExecutionContext is destroyed");
+  wgx_ctx* c = new wgx_ctx();
+  c->d = parent->d;
+  c->d->refs++;
   *out = c;
   return WGX_OK;
 }
 
 void wgx_ctx_destroy(wgx_ctx* c) {
   if (!c) return;
-  if (c->has_dev) {
-    hipSetDevice(c->device);
-    hipStreamSynchronize(c->stream);
+  DeviceState* ds = c->d;
+  if (ds->has_dev) {
+    hipSetDevice(ds->device);
+    hipStreamSynchronize(ds->stream);
   }
   c->invalidate();
-  for (auto& kv : c->bufs) {
-    if (c->has_dev)
-      hipFree(reinterpret_cast<void*>(kv.first));
-    else
-      free(reinterpret_cast<void*>(kv.first));
+  std::vector<uintptr_t> mine;
+  for (auto& kv : ds->bufs)
+    if (kv.second.owner == c) mine.push_back(kv.first);
+  for (uintptr_t b : mine) c->release(b);
+  if (--ds->refs == 0) {
+    std::vector<uintptr_t> rest;
+    for (auto& kv : ds->bufs) rest.push_back(kv.first);
+    for (uintptr_t b : rest) c->release(b);
+    if (ds->has_dev && ds->stream) hipStreamDestroy(ds->stream);
+    delete ds;
   }
-  c->bufs.clear();
-  if (c->has_dev && c->stream) hipStreamDestroy(c->stream);
   delete c;
 }
 
+int wgx_free(wgx_ctx* c, void* ptr) {
+  CTX_GUARD(c);
+  auto it = c->d->bufs.find(reinterpret_cast<uintptr_t>(ptr));
+  if (it == c->d->bufs.end()) return c->fail(WGX_ERR_INVALID, "free: %p is not a buffer of this device", ptr);
+  if (c->d->has_dev) {
+    hipError_t e = hipStreamSynchronize(c->d->stream);
+    if (e != hipSuccess) return c->hip_fail(e, "free");
+  }
+  c->release(it->first);
+  return WGX_OK;
+}
+
 const char* wgx_last_error(const wgx_ctx* c) { return c ? c->err.c_str() : "null context"; }
-int wgx_ctx_has_device(const wgx_ctx* c) { return c && c->has_dev ? 1 : 0; }
-const char* wgx_ctx_arch(const wgx_ctx* c) { return c ? c->arch.c_str() : ""; }
-void* wgx_ctx_stream(const wgx_ctx* c) { return c ? (void*)c->stream : nullptr; }
+int wgx_ctx_has_device(const wgx_ctx* c) { return c && c->d->has_dev ? 1 : 0; }
+const char* wgx_ctx_arch(const wgx_ctx* c) { return c ? c->d->arch.c_str() : ""; }
+void* wgx_ctx_stream(const wgx_ctx* c) { return c ? (void*)c->d->stream : nullptr; }
 const char* wgx_last_kernel(const wgx_ctx* c) { return c ? c->last_kernel.c_str() : ""; }
 int wgx_command_count(const wgx_ctx* c) { return c ? (int)c->cmds.size() : 0; }
 
@@ -241,7 +315,7 @@ int wgx_alloc(wgx_ctx* c, uint64_t bytes, uint32_t usage, void** out) {
   const uint64_t sz = bytes < 4 ? 4 : (bytes + 3) / 4 * 4;
   void* p = c->owned_alloc(sz);
   if (!p) return c->fail(WGX_ERR_OOM, "alloc: could not allocate %llu bytes", (unsigned long long)sz);
-  c->bufs[reinterpret_cast<uintptr_t>(p)].usage = usage;
+  c->d->bufs[reinterpret_cast<uintptr_t>(p)].usage = usage;
   *out = p;
   return WGX_OK;
 }
@@ -262,12 +336,12 @@ int wgx_write(wgx_ctx* c, void* dst, const void* src, uint64_t bytes) {
   CTX_GUARD(c);
   if (bytes == 0) return WGX_OK;
   if (!c->find(dst, bytes)) return c->fail(WGX_ERR_INVALID, "write: destination range is not an owned buffer");
-  if (!c->has_dev) {
+  if (!c->d->has_dev) {
     memcpy(dst, src, bytes);
     return WGX_OK;
   }
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->d->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->d->stream);
   return e == hipSuccess ? WGX_OK : c->hip_fail(e, "write");
 }
 
@@ -275,19 +349,19 @@ int wgx_read(wgx_ctx* c, const void* src, void* dst, uint64_t bytes) {
   CTX_GUARD(c);
   if (bytes == 0) return WGX_OK;
   if (!c->find(src, bytes)) return c->fail(WGX_ERR_INVALID, "read: source range is not an owned buffer");
-  if (!c->has_dev) {
+  if (!c->d->has_dev) {
     memcpy(dst, src, bytes);
     return WGX_OK;
   }
-  hipError_t e = hipStreamSynchronize(c->stream);
+  hipError_t e = hipStreamSynchronize(c->d->stream);
   if (e == hipSuccess) e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
   return e == hipSuccess ? WGX_OK : c->hip_fail(e, "read");
 }
 
 int wgx_record_copy(wgx_ctx* c, void* dst, const void* src, uint64_t bytes) {
   CTX_GUARD(c);
-  if (!c->find(src, bytes)) return c->fail(WGX_ERR_INVALID, "copy: source range is not an owned buffer");
-  if (!c->find(dst, bytes)) return c->fail(WGX_ERR_INVALID, "copy: destination range is not an owned buffer");
+  if (!c->use(src, bytes)) return c->fail(WGX_ERR_INVALID, "copy: source range is not an owned buffer");
+  if (!c->use(dst, bytes)) return c->fail(WGX_ERR_INVALID, "copy: destination range is not an owned buffer");
   if (bytes == 0 || src == dst) {
     c->last_kernel = "copy_elided";
     return WGX_OK;
@@ -527,7 +601,7 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
       conv_fill_ktab(tab.data(), d.K, (int)IC, d.g);
       void* dev = c->owned_alloc(sizeof(uint32_t) * rows);
       if (!dev) return c->fail(WGX_ERR_OOM, "convolution: im2col table allocation failed");
-      if (c->has_dev) {
+      if (c->d->has_dev) {
         e = hipMemcpy(dev, tab.data(), sizeof(uint32_t) * rows, hipMemcpyHostToDevice);
         if (e != hipSuccess) return c->hip_fail(e, "convolution: im2col table upload");
       } else {
@@ -760,7 +834,7 @@ int wgx_record_max_pool2d(wgx_ctx* c, const wgx_tensor* in, const int32_t kernel
 
 static int run_eager(wgx_ctx* c) {
   for (const Cmd& cmd : c->cmds) {
-    hipError_t e = cmd.fn(c->stream);
+    hipError_t e = cmd.fn(c->d->stream);
     if (e != hipSuccess) return c->hip_fail(e, cmd.name.c_str());
   }
   return WGX_OK;
@@ -769,21 +843,22 @@ static int run_eager(wgx_ctx* c) {
 int wgx_submit(wgx_ctx* c) {
   CTX_GUARD(c);
   if (c->cmds.empty()) return WGX_OK;
-  if (!c->has_dev) return c->fail(WGX_ERR_NO_DEVICE, "submit: host-only context has no device");
+  if (!c->d->has_dev) return c->fail(WGX_ERR_NO_DEVICE, "submit: host-only context has no device");
+  if (int r = c->check_uses()) return r;
   if (!c->graph_mode) return run_eager(c);
   if (!c->graph_valid) {
-    hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    hipError_t e = hipStreamBeginCapture(c->d->stream, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) return c->hip_fail(e, "submit: begin capture");
     int r = WGX_OK;
     for (const Cmd& cmd : c->cmds) {
-      e = cmd.fn(c->stream);
+      e = cmd.fn(c->d->stream);
       if (e != hipSuccess) {
         r = c->hip_fail(e, cmd.name.c_str());
         break;
       }
     }
     hipGraph_t g = nullptr;
-    hipError_t e2 = hipStreamEndCapture(c->stream, &g);
+    hipError_t e2 = hipStreamEndCapture(c->d->stream, &g);
     if (r != WGX_OK) {
       if (g) hipGraphDestroy(g);
       return r;
@@ -797,14 +872,14 @@ int wgx_submit(wgx_ctx* c) {
     }
     c->graph_valid = true;
   }
-  hipError_t e = hipGraphLaunch(c->exec, c->stream);
+  hipError_t e = hipGraphLaunch(c->exec, c->d->stream);
   return e == hipSuccess ? WGX_OK : c->hip_fail(e, "submit: graph launch");
 }
 
 int wgx_sync(wgx_ctx* c) {
   CTX_GUARD(c);
-  if (!c->has_dev) return WGX_OK;
-  hipError_t e = hipStreamSynchronize(c->stream);
+  if (!c->d->has_dev) return WGX_OK;
+  hipError_t e = hipStreamSynchronize(c->d->stream);
   return e == hipSuccess ? WGX_OK : c->hip_fail(e, "sync");
 }
 
@@ -824,7 +899,7 @@ int wgx_set_graph_mode(wgx_ctx* c, int enabled) {
 
 int wgx_time_submits(wgx_ctx* c, int reps, float* ms_per_submit) {
   CTX_GUARD(c);
-  if (!c->has_dev) return c->fail(WGX_ERR_NO_DEVICE, "time: host-only context has no device");
+  if (!c->d->has_dev) return c->fail(WGX_ERR_NO_DEVICE, "time: host-only context has no device");
   if (reps <= 0 || !ms_per_submit) return c->fail(WGX_ERR_INVALID, "time: reps must be positive");
   hipEvent_t a, b;
   hipError_t e = hipEventCreate(&a);
@@ -835,9 +910,9 @@ int wgx_time_submits(wgx_ctx* c, int reps, float* ms_per_submit) {
     return c->hip_fail(e, "time: event");
   }
   int r = WGX_OK;
-  e = hipEventRecord(a, c->stream);
+  e = hipEventRecord(a, c->d->stream);
   for (int i = 0; i < reps && e == hipSuccess && r == WGX_OK; ++i) r = wgx_submit(c);
-  if (e == hipSuccess && r == WGX_OK) e = hipEventRecord(b, c->stream);
+  if (e == hipSuccess && r == WGX_OK) e = hipEventRecord(b, c->d->stream);
   if (e == hipSuccess && r == WGX_OK) e = hipEventSynchronize(b);
   float ms = 0.f;
   if (e == hipSuccess && r == WGX_OK) e = hipEventElapsedTime(&ms, a, b);

@@ -1,0 +1,463 @@
+'use strict';
+/**
+ * Node host layer of wgpu-executorch_amd: the reference's public API for the
+ * GEMM-shaped hot path (src/tensor.ts, src/context.ts, src/shader.ts,
+ * src/program.ts, src/shaders/index.ts), executing through libwgx (the
+ * MI355X C-ABI in include/wgx.h) via the N-API addon wgx_napi.node.
+ *
+ * Written as ES2019 CommonJS because this image's Node is v12 and has no
+ * TypeScript compiler; index.d.ts carries the types.  Validation and error
+ * texts follow the reference drivers so code and tests written against the
+ * reference behave the same; the C library re-validates every record
+ * against the buffers it owns, so no launch can address memory outside them.
+ */
+const path = require('path');
+const native = require(path.join(__dirname, 'wgx_napi.node'));
+
+// ------------------------------------------------------------------ tensor.ts
+
+/** GPUBufferUsage flags (WebGPU values). */
+const GPUBufferUsage = Object.freeze({
+  MAP_READ: 0x1, MAP_WRITE: 0x2, COPY_SRC: 0x4, COPY_DST: 0x8, INDEX: 0x10, VERTEX: 0x20,
+  UNIFORM: 0x40, STORAGE: 0x80, INDIRECT: 0x100, QUERY_RESOLVE: 0x200,
+});
+
+/** src/tensor.ts:57 */
+const MAX_NDIM = 8;
+
+/** src/tensor.ts:60-64, plus bfloat16. */
+const DTYPE_BYTESIZE = Object.freeze({
+  float32: 4, float16: 2, float64: 8, int32: 4, int64: 8, int8: 1, uint8: 1, bool: 1, bfloat16: 2,
+});
+const DTYPE_CODE = Object.freeze({
+  float32: 0, float16: 1, int32: 2, int8: 3, uint8: 4, bool: 5, float64: 6, int64: 7, bfloat16: 8,
+});
+
+const STORAGE_BUFFER_USAGE = GPUBufferUsage.STORAGE | GPUBufferUsage.COPY_SRC | GPUBufferUsage.COPY_DST;
+const UNIFORM_BUFFER_USAGE = GPUBufferUsage.UNIFORM | GPUBufferUsage.COPY_DST;
+
+/**
+ * A device allocation (the GPUBuffer stand-in).  `ptr` is the HIP device
+ * address; `view(offset, size)` makes a sub-range that tensors can wrap
+ * (used for memory-plan pools carved out of one allocation).
+ */
+class WgxBuffer {
+  constructor(device, ptr, size, usage, base) {
+    this._device = device;
+    this.ptr = ptr;
+    this.size = size;
+    this.usage = usage;
+    this._base = base || null;
+    this._destroyed = false;
+  }
+
+  view(offset, size) {
+    return new WgxBuffer(this._device, this.ptr + offset, size, this.usage, this._base || this);
+  }
+
+  destroy() {
+    if (this._destroyed || this._base || this.ptr === 0) return;
+    this._destroyed = true;
+    native.free(this._device._h, this.ptr);
+  }
+}
+
+/**
+ * One GPU (the GPUDevice stand-in).  It owns the device-wide buffer
+ * registry and the queue (one HIP stream): every WgpuExecutionContext made
+ * on it submits to that queue in order.
+ */
+class WgxDevice {
+  constructor(index) {
+    this._h = native.ctxCreate(index);
+    const info = native.ctxInfo(this._h);
+    this.index = index;
+    this.arch = info.arch;
+    this.features = new Set(['shader-f16']);
+    const self = this;
+    this.queue = {
+      writeBuffer(buffer, offset, data, dataOffset, size) {
+        const ab = data instanceof ArrayBuffer ? data : data.buffer;
+        const base = data instanceof ArrayBuffer ? 0 : data.byteOffset;
+        native.write(self._h, buffer.ptr + (offset || 0), ab, base + (dataOffset || 0),
+          size === undefined ? ab.byteLength - base - (dataOffset || 0) : size);
+      },
+      onSubmittedWorkDone() {
+        native.sync(self._h);
+        return Promise.resolve();
+      },
+    };
+  }
+
+  /** device.createBuffer({size, usage}): a device allocation the caller owns. */
+  createBuffer(desc) {
+    const size = Math.max(4, Math.ceil(desc.size / 4) * 4);
+    const ptr = native.alloc(this._h, size, desc.usage);
+    return new WgxBuffer(this, ptr, desc.size, desc.usage);
+  }
+
+  destroy() {
+    if (this._h) native.ctxDestroy(this._h);
+    this._h = null;
+  }
+}
+
+/** Opens GPU `index` (HIP device ordinal); -1 gives a host-only validation device. */
+async function requestDevice(index) {
+  return new WgxDevice(index === undefined ? 0 : index);
+}
+
+function createDevice(index) {
+  return new WgxDevice(index === undefined ? 0 : index);
+}
+
+/** A non-owning tensor view (src/tensor.ts:77-193). */
+class Tensor {
+  constructor(dtype, shape, device, buffer) {
+    if (shape.length > MAX_NDIM) {
+      throw new Error(`Tensor rank ${shape.length} exceeds maximum rank of ${MAX_NDIM}`);
+    }
+    if (shape.some((dim) => dim <= 0 || !Number.isInteger(dim))) {
+      throw new Error('Tensor dimensions must be positive integers');
+    }
+    this._dtype = dtype;
+    this._shape = shape;
+    this._numel = shape.reduce((a, b) => a * b, 1);
+    this._buffer = buffer;
+    this._device = device;
+    const requiredBytes = this._numel * DTYPE_BYTESIZE[dtype];
+    if (buffer.size < requiredBytes) {
+      throw new Error(`GPUBuffer size (${buffer.size}B) < required (${requiredBytes}B)`);
+    }
+    if ((buffer.usage & GPUBufferUsage.STORAGE) === 0) {
+      throw new Error('GPUBuffer must have GPUBufferUsage.STORAGE flag');
+    }
+  }
+
+  get dtype() { return this._dtype; }
+  get numel() { return this._numel; }
+  get shape() { return this._shape; }
+  get buffer() { return this._buffer; }
+  get device() { return this._device; }
+  get byteLength() { return this._numel * DTYPE_BYTESIZE[this._dtype]; }
+
+  /** {ptr, dtype, shape} for the native records. */
+  _c() {
+    return { ptr: this._buffer.ptr, dtype: DTYPE_CODE[this._dtype], shape: this._shape };
+  }
+
+  /** src/tensor.ts:149-169: prefix write, padded to 4 bytes. */
+  setData(src) {
+    const byteLength = this.byteLength;
+    if ((this._buffer.usage & GPUBufferUsage.COPY_DST) === 0) {
+      throw new Error('setData: buffer missing COPY_DST usage');
+    }
+    if (src.byteLength > byteLength) {
+      throw new Error(`setData: source ${src.byteLength}B > tensor ${byteLength}B; pass a view`);
+    }
+    const alignedSize = Math.min(Math.ceil(src.byteLength / 4) * 4, this._buffer.size);
+    const bytes = new Uint8Array(Math.ceil(src.byteLength / 4) * 4);
+    bytes.set(src instanceof ArrayBuffer
+      ? new Uint8Array(src, 0, src.byteLength)
+      : new Uint8Array(src.buffer, src.byteOffset, src.byteLength));
+    native.write(this._device._h, this._buffer.ptr, bytes.buffer, 0, alignedSize);
+    return this;
+  }
+
+  /** src/tensor.ts:176-192: waits for submitted work, resolves the bytes. */
+  async getData() {
+    return native.read(this._device._h, this._buffer.ptr, this.byteLength);
+  }
+}
+
+// ------------------------------------------------------------------ context.ts
+
+/** Execution context (src/context.ts:17-390). */
+class WgpuExecutionContext {
+  constructor(device) {
+    this._device = device;
+    this._h = native.ctxCreateShared(device._h);
+    this._destroyed = false;
+  }
+
+  get device() { return this._device; }
+
+  _assertNotDestroyed() {
+    if (this._destroyed) throw new Error('WgpuExecutionContext is destroyed');
+  }
+
+  destroy() {
+    if (this._destroyed) return;
+    this._destroyed = true;
+    native.ctxDestroy(this._h);  // frees every buffer this context allocated
+  }
+
+  storageBuffer(size) {
+    this._assertNotDestroyed();
+    const alignedSize = Math.max(4, Math.ceil(size / 4) * 4);
+    const ptr = native.alloc(this._h, alignedSize, STORAGE_BUFFER_USAGE);
+    return new WgxBuffer(this._device, ptr, alignedSize, STORAGE_BUFFER_USAGE);
+  }
+
+  /**
+   * Parameters reach the kernels by value here, so a uniform buffer is a
+   * host-side record of its bytes (kept for API compatibility).
+   */
+  uniformBuffer(data) {
+    this._assertNotDestroyed();
+    const bytes = data instanceof ArrayBuffer ? data.slice(0) : data.buffer.slice(data.byteOffset, data.byteOffset + data.byteLength);
+    const buf = new WgxBuffer(this._device, 0, Math.max(16, Math.ceil(bytes.byteLength / 4) * 4), UNIFORM_BUFFER_USAGE);
+    buf.data = bytes;
+    return buf;
+  }
+
+  tensor(dtype, shape, buffer) {
+    this._assertNotDestroyed();
+    if (buffer !== undefined) return new Tensor(dtype, shape, this._device, buffer);
+    const numel = shape.reduce((a, b) => a * b, 1);
+    return new Tensor(dtype, shape, this._device, this.storageBuffer(numel * DTYPE_BYTESIZE[dtype]));
+  }
+
+  /** Raw WebGPU dispatch descriptors have no equivalent here (no WGSL pipelines). */
+  addDispatch() {
+    this._assertNotDestroyed();
+    throw new Error('addDispatch: WebGPU pipelines do not exist on the MI355X backend; record operators with recordShader');
+  }
+
+  copy(src, dst) {
+    this._assertNotDestroyed();
+    if ((src.buffer.usage & GPUBufferUsage.COPY_SRC) === 0) {
+      throw new Error('copy: source buffer missing COPY_SRC usage');
+    }
+    if ((dst.buffer.usage & GPUBufferUsage.COPY_DST) === 0) {
+      throw new Error('copy: destination buffer missing COPY_DST usage');
+    }
+    if (dst.byteLength < src.byteLength) {
+      throw new Error(`copy: destination (${dst.byteLength}B) < source (${src.byteLength}B)`);
+    }
+    native.recordCopy(this._h, dst.buffer.ptr, src.buffer.ptr, src.byteLength);
+    return this;
+  }
+
+  recordShader(shader, args) {
+    this._assertNotDestroyed();
+    shader.recordIn(this, args);
+    return this;
+  }
+
+  /**
+   * src/context.ts:219-317.  Memory-plan pools become views into ONE device
+   * allocation (256-byte aligned offsets) and constants into one weights
+   * allocation, instead of one buffer per pool / per constant.
+   */
+  recordProgram(program, weights, args) {
+    this._assertNotDestroyed();
+    const numInputs = program.inputIds.length;
+    const numOutputs = program.outputIds.length;
+    if (args.length !== numInputs + numOutputs) {
+      throw new Error(`program: expected ${numInputs + numOutputs} args, got ${args.length}`);
+    }
+    const align = (n) => Math.ceil(n / 256) * 256;
+
+    // pools -> one slab
+    const poolOffset = new Map();
+    let poolBytes = 0;
+    for (const pool of program.memoryPlan.pools) {
+      poolOffset.set(pool.id, { off: poolBytes, size: Math.max(4, Math.ceil(pool.size / 4) * 4) });
+      poolBytes += align(Math.max(4, pool.size));
+    }
+    const poolSlab = poolBytes > 0 ? this.storageBuffer(poolBytes) : null;
+
+    // constants -> one slab (each constant realigned to 256 bytes)
+    const constOffset = new Map();
+    let constBytes = 0;
+    program.values.forEach((v, i) => {
+      if (v.type === 'tensor' && v.weightsOffset !== undefined && v.weightsLength !== undefined) {
+        constOffset.set(i, constBytes);
+        constBytes += align(Math.max(4, v.weightsLength));
+      }
+    });
+    const constSlab = constBytes > 0 ? this.storageBuffer(constBytes) : null;
+
+    const tensors = new Map();
+    program.values.forEach((v, i) => {
+      if (v.type !== 'tensor') return;
+      let buffer;
+      if (v.weightsOffset !== undefined && v.weightsLength !== undefined) {
+        buffer = constSlab.view(constOffset.get(i), Math.max(4, Math.ceil(v.weightsLength / 4) * 4));
+      } else if (v.memObjId !== undefined) {
+        if (!poolOffset.has(v.memObjId)) {
+          throw new Error(`program: no memory pool ${v.memObjId} for value ${i}`);
+        }
+        const p = poolOffset.get(v.memObjId);
+        buffer = poolSlab.view(p.off, p.size);
+      } else {
+        const numel = v.shape.reduce((a, b) => a * b, 1);
+        buffer = this.storageBuffer(numel * DTYPE_BYTESIZE[v.dtype]);
+      }
+      tensors.set(i, this.tensor(v.dtype, v.shape, buffer));
+    });
+
+    // weights: one staging image of the constant slab, one upload
+    if (constSlab) {
+      const staging = new Uint8Array(constBytes);
+      const src = weights instanceof ArrayBuffer ? new Uint8Array(weights)
+        : new Uint8Array(weights.buffer, weights.byteOffset, weights.byteLength);
+      program.values.forEach((v, i) => {
+        if (constOffset.has(i)) {
+          staging.set(src.subarray(v.weightsOffset, v.weightsOffset + v.weightsLength), constOffset.get(i));
+        }
+      });
+      native.write(this._device._h, constSlab.ptr, staging.buffer, 0, constBytes);
+    }
+
+    for (let i = 0; i < numInputs; i++) {
+      const src = args[i];
+      const dst = tensors.get(program.inputIds[i]);
+      if (!(src instanceof Tensor)) continue;
+      if (dst === undefined) throw new Error(`program: no tensor for input value ${program.inputIds[i]}`);
+      this.copy(src, dst);
+    }
+
+    for (const op of program.chain) {
+      const shader = shaderRegistry[op.name];
+      if (!shader) throw new Error(`program: unknown operator '${op.name}'`);
+      this.recordShader(shader, resolveArgs(op, program.values, tensors));
+    }
+
+    for (let i = 0; i < numOutputs; i++) {
+      const src = tensors.get(program.outputIds[i]);
+      const dst = args[numInputs + i];
+      if (!(dst instanceof Tensor)) throw new Error(`program: output ${i} must be a Tensor`);
+      if (src === undefined) throw new Error(`program: no tensor for output value ${program.outputIds[i]}`);
+      this.copy(src, dst);
+    }
+    return this;
+  }
+
+  submit() {
+    this._assertNotDestroyed();
+    native.submit(this._h);
+  }
+
+  async sync() {
+    this._assertNotDestroyed();
+    native.sync(this._h);
+  }
+
+  reset() {
+    this._assertNotDestroyed();
+    native.reset(this._h);
+  }
+
+  /** Extras of this backend: replay through a HIP graph (default) or eagerly. */
+  setGraphMode(enabled) { native.setGraphMode(this._h, enabled ? 1 : 0); }
+
+  /** Mean device time of `reps` back-to-back submits, HIP events on the queue. */
+  timeSubmits(reps) { return native.timeSubmits(this._h, reps); }
+
+  /** Kernel chosen by the most recent record. */
+  get lastKernel() { return native.ctxInfo(this._h).lastKernel; }
+
+  get commandCount() { return native.ctxInfo(this._h).commandCount; }
+}
+
+// ------------------------------------------------------------------ program.ts
+
+/** src/program.ts:188-224 */
+function resolveArgs(op, values, tensors) {
+  return op.args.map((idx) => {
+    const v = values[idx];
+    switch (v.type) {
+      case 'tensor': {
+        const t = tensors.get(idx);
+        if (t === undefined) throw new Error(`program: no tensor for value ${idx} referenced by '${op.name}'`);
+        return t;
+      }
+      case 'scalar':
+        return v.value;
+      case 'list':
+        return v.items.slice();
+      case 'tensorlist':
+        return v.items.map((j) => {
+          const item = values[j];
+          if (!item || item.type !== 'tensor') {
+            throw new Error(`program: tensorlist item ${j} is not a tensor (${op.name})`);
+          }
+          const t = tensors.get(j);
+          if (t === undefined) throw new Error(`program: no tensor for value ${j} referenced by '${op.name}'`);
+          return t;
+        });
+      case 'null':
+        return undefined;
+      default:
+        return undefined;
+    }
+  });
+}
+
+// ------------------------------------------------------------------ operators
+
+const shaders = require('./shaders')({ native, Tensor, DTYPE_BYTESIZE });
+
+/** src/shaders/index.ts:58-60 */
+const shaderRegistry = Object.fromEntries
+  ? Object.fromEntries(Object.values(shaders).map((s) => [s.name, s]))
+  : Object.values(shaders).reduce((o, s) => { o[s.name] = s; return o; }, {});
+
+// ------------------------------------------------------------------ float16 helpers
+// Node 12 has no Float16Array: f16 data crosses as Uint16Array bit patterns.
+
+const f32buf = new Float32Array(1);
+const u32buf = new Uint32Array(f32buf.buffer);
+
+/** float -> IEEE binary16 bits, round to nearest even. */
+function toHalf(f) {
+  f32buf[0] = f;
+  const x = u32buf[0];
+  const sign = (x >>> 16) & 0x8000;
+  const ax = x & 0x7fffffff;
+  if (ax >= 0x7f800000) return sign | (ax > 0x7f800000 ? 0x7e00 : 0x7c00);
+  if (ax >= 0x477ff000) return sign | 0x7c00;
+  if (ax < 0x38800000) {
+    f32buf[0] = Math.abs(f) * 16777216;
+    const s = f32buf[0];
+    let m = Math.floor(s);
+    const r = s - m;
+    if (r > 0.5 || (r === 0.5 && (m & 1))) m += 1;
+    return sign | m;
+  }
+  let h = (((ax >>> 23) - 112) << 10) | ((ax >>> 13) & 0x3ff);
+  const rem = ax & 0x1fff;
+  if (rem > 0x1000 || (rem === 0x1000 && (h & 1))) h += 1;
+  return sign | h;
+}
+
+function fromHalf(h) {
+  const e = (h >>> 10) & 0x1f;
+  const m = h & 0x3ff;
+  let v;
+  if (e === 0) v = m * Math.pow(2, -24);
+  else if (e === 31) v = m ? NaN : Infinity;
+  else v = (m + 1024) * Math.pow(2, e - 25);
+  return (h & 0x8000) ? -v : v;
+}
+
+function toFloat16Array(values) {
+  const out = new Uint16Array(values.length);
+  for (let i = 0; i < values.length; i++) out[i] = toHalf(values[i]);
+  return out;
+}
+
+function fromFloat16Array(bits) {
+  const u = bits instanceof ArrayBuffer ? new Uint16Array(bits) : bits;
+  const out = new Float32Array(u.length);
+  for (let i = 0; i < u.length; i++) out[i] = fromHalf(u[i]);
+  return out;
+}
+
+module.exports = {
+  GPUBufferUsage, MAX_NDIM, DTYPE_BYTESIZE, Tensor, WgpuExecutionContext, WgxDevice, WgxBuffer,
+  requestDevice, createDevice, resolveArgs, shaders, shaderRegistry, toHalf, fromHalf,
+  toFloat16Array, fromFloat16Array,
+};

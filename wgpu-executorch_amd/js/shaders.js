@@ -1,0 +1,357 @@
+'use strict';
+/**
+ * Operator drivers (the Shader objects of src/shaders/<op>/index.ts):
+ * `{ name, code, recordIn(ctx, args) }`.  Each recordIn validates its
+ * argument tuple with the reference's checks and messages, then appends one
+ * native record.  `code` names the MI355X kernels instead of holding WGSL.
+ */
+module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
+  const isFloatPair = (t) => t.dtype === 'float32' || t.dtype === 'float16';
+
+  function parseHw(name, v, argName) {
+    if (v.length === 1) return [v[0], v[0]];
+    if (v.length === 2) return [v[0], v[1]];
+    throw new Error(`${name}: ${argName} must be 1 or 2 elements`);
+  }
+
+  function broadcastable(a, b, out) {
+    const n = out.shape.length;
+    if (a.shape.length > n || b.shape.length > n) return false;
+    for (let k = 0; k < n; k++) {
+      const o = out.shape[n - 1 - k];
+      const da = k < a.shape.length ? a.shape[a.shape.length - 1 - k] : 1;
+      const db = k < b.shape.length ? b.shape[b.shape.length - 1 - k] : 1;
+      if ((da !== o && da !== 1) || (db !== o && db !== 1)) return false;
+    }
+    return true;
+  }
+
+  // ---------------------------------------------------------------- mm (src/shaders/mm/index.ts:32-93)
+  const mm = {
+    name: 'aten.mm.default',
+    code: { f32: 'gemm_f32 (vector FMA, LDS-blocked)', f16: 'gemm_mfma (v_mfma_f32_32x32x16_f16)' },
+    recordIn(ctx, [in1, in2, out]) {
+      const name = 'aten.mm.default';
+      if (!isFloatPair(in1) || in2.dtype !== in1.dtype || out.dtype !== in1.dtype) {
+        throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+      }
+      if (in1.shape.length !== 2 || in2.shape.length !== 2 || out.shape.length !== 2) {
+        throw new Error(`${name}: Tensors must be 2D matrices`);
+      }
+      const [m, k1] = in1.shape;
+      const [k2, n] = in2.shape;
+      const [outM, outN] = out.shape;
+      if (k1 !== k2) throw new Error(`${name}: Matrix inner dimensions must match (${k1} !== ${k2})`);
+      if (outM !== m || outN !== n) {
+        throw new Error(`${name}: Output shape [${outM}, ${outN}] !== expected [${m}, ${n}]`);
+      }
+      native.recordMm(ctx._h, in1._c(), in2._c(), null, out._c(), 1, 1, 0);
+    },
+  };
+
+  // ---------------------------------------------------------------- addmm (new: absent from the reference)
+  // aten.addmm.default [bias, mat1, mat2, beta?, alpha?, out]: out = beta*bias + alpha*(mat1 @ mat2)
+  const addmm = {
+    name: 'aten.addmm.default',
+    code: { f16: 'gemm_mfma with fused bias epilogue' },
+    recordIn(ctx, args) {
+      const name = 'aten.addmm.default';
+      const [bias, mat1, mat2] = args;
+      const out = args[args.length - 1];
+      const beta = args.length >= 5 && typeof args[3] === 'number' ? args[3] : 1;
+      const alpha = args.length >= 6 && typeof args[4] === 'number' ? args[4] : 1;
+      if (!isFloatPair(mat1) || mat2.dtype !== mat1.dtype || out.dtype !== mat1.dtype || bias.dtype !== mat1.dtype) {
+        throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+      }
+      if (mat1.shape.length !== 2 || mat2.shape.length !== 2 || out.shape.length !== 2) {
+        throw new Error(`${name}: Tensors must be 2D matrices`);
+      }
+      const [m, k1] = mat1.shape;
+      const [k2, n] = mat2.shape;
+      if (k1 !== k2) throw new Error(`${name}: Matrix inner dimensions must match (${k1} !== ${k2})`);
+      if (out.shape[0] !== m || out.shape[1] !== n) {
+        throw new Error(`${name}: Output shape [${out.shape[0]}, ${out.shape[1]}] !== expected [${m}, ${n}]`);
+      }
+      native.recordMm(ctx._h, mat1._c(), mat2._c(), bias._c(), out._c(), alpha, beta, 0);
+    },
+  };
+
+  // Linear layer with the nn.Linear weight layout W[N,K]: [x, weight, bias|undefined, out]
+  const linear = {
+    name: 'aten.linear.default',
+    code: { f16: 'gemm_mfma NT form (k-contiguous weight rows)' },
+    recordIn(ctx, [x, weight, bias, out]) {
+      const name = 'aten.linear.default';
+      if (!isFloatPair(x) || weight.dtype !== x.dtype || out.dtype !== x.dtype) {
+        throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+      }
+      if (x.shape.length !== 2 || weight.shape.length !== 2 || out.shape.length !== 2) {
+        throw new Error(`${name}: Tensors must be 2D matrices`);
+      }
+      if (x.shape[1] !== weight.shape[1]) {
+        throw new Error(`${name}: Matrix inner dimensions must match (${x.shape[1]} !== ${weight.shape[1]})`);
+      }
+      native.recordMm(ctx._h, x._c(), weight._c(), bias === undefined ? null : bias._c(), out._c(), 1, 1, 1);
+    },
+  };
+
+  // ---------------------------------------------------------------- bmm (src/shaders/bmm/index.ts:27-96)
+  const bmm = {
+    name: 'aten.bmm.default',
+    code: { f32: 'gemm_f32 batched', f16: 'gemm_mfma batched' },
+    recordIn(ctx, [a, b, out]) {
+      const name = 'aten.bmm.default';
+      if (!isFloatPair(a) || b.dtype !== a.dtype || out.dtype !== a.dtype) {
+        throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+      }
+      if (a.shape.length !== 3 || b.shape.length !== 3 || out.shape.length !== 3) {
+        throw new Error(`${name}: inputs and output must be 3D`);
+      }
+      const [batch, m, k] = a.shape;
+      const n = b.shape[2];
+      if (b.shape[0] !== batch || b.shape[1] !== k) throw new Error(`${name}: batch/K mismatch between a and b`);
+      if (out.shape[0] !== batch || out.shape[1] !== m || out.shape[2] !== n) {
+        throw new Error(`${name}: output shape [${out.shape}] != [${batch}, ${m}, ${n}]`);
+      }
+      native.recordBmm(ctx._h, a._c(), b._c(), out._c(), 0);
+    },
+  };
+
+  // ---------------------------------------------------------------- convolution (src/shaders/convolution/index.ts:58-310)
+  function recordConv(name, ctx, inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding,
+    groups, outTensor, clampMin, clampMax) {
+    if (!isFloatPair(inTensor) || weight.dtype !== inTensor.dtype || outTensor.dtype !== inTensor.dtype) {
+      throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+    }
+    if (bias !== undefined && bias.dtype !== inTensor.dtype) {
+      throw new Error(`${name}: bias dtype must match input dtype`);
+    }
+    if (inTensor.shape.length !== 4 || weight.shape.length !== 4 || outTensor.shape.length !== 4) {
+      throw new Error(`${name}: expected 4D tensors for input, weight, and output`);
+    }
+    const [sH, sW] = parseHw(name, stride, 'stride');
+    const [pH, pW] = parseHw(name, padding, 'padding');
+    const [dH, dW] = parseHw(name, dilation, 'dilation');
+    const [opH, opW] = parseHw(name, outputPadding, 'output_padding');
+    const [, ic, ih, iw] = inTensor.shape;
+    const kh = weight.shape[2];
+    const kw = weight.shape[3];
+    if (transposed) {
+      if (weight.shape[0] !== ic) throw new Error(`${name}: weight dim0 !== IC (${weight.shape[0]} != ${ic})`);
+      if (opH >= sH || opW >= sW) throw new Error(`${name}: output_padding >= stride`);
+      const eoh = (ih - 1) * sH - 2 * pH + dH * (kh - 1) + opH + 1;
+      const eow = (iw - 1) * sW - 2 * pW + dW * (kw - 1) + opW + 1;
+      if (outTensor.shape[2] !== eoh || outTensor.shape[3] !== eow) {
+        throw new Error(`${name}: expected output spatial [${eoh}, ${eow}]`);
+      }
+    } else {
+      if (outputPadding.some((v) => v !== 0)) {
+        throw new Error(`${name}: non-zero output_padding unsupported for non-transposed conv`);
+      }
+      if (weight.shape[1] !== ic / groups) {
+        throw new Error(`${name}: weight in-ch (${weight.shape[1]}) != IC/groups (${ic / groups})`);
+      }
+      const ohNum = ih + 2 * pH - dH * (kh - 1) - 1;
+      const owNum = iw + 2 * pW - dW * (kw - 1) - 1;
+      if (ohNum < 0 || owNum < 0) throw new Error(`${name}: invalid geometry (kernel larger than input)`);
+      const eoh = Math.floor(ohNum / sH) + 1;
+      const eow = Math.floor(owNum / sW) + 1;
+      if (outTensor.shape[2] !== eoh || outTensor.shape[3] !== eow) {
+        throw new Error(`${name}: expected output spatial [${eoh}, ${eow}]`);
+      }
+    }
+    const hasClamp = clampMin !== undefined || clampMax !== undefined;
+    native.recordConv2d(ctx._h, inTensor._c(), weight._c(), bias === undefined ? null : bias._c(), {
+      stride: [sH, sW], padding: [pH, pW], dilation: [dH, dW], outputPadding: [opH, opW],
+      transposed: transposed ? 1 : 0, groups, hasClamp: hasClamp ? 1 : 0,
+      clampMin: clampMin === undefined ? -Infinity : clampMin,
+      clampMax: clampMax === undefined ? Infinity : clampMax,
+    }, outTensor._c());
+  }
+
+  const convolution = {
+    name: 'aten.convolution.default',
+    code: {
+      gemm: 'gemm_mfma / gemm_f32 implicit-im2col (B_CONV) and 1x1 (B_KN)',
+      depthwise: 'depthwise (LDS-banded stencil)', fallback: 'conv_grouped_direct / conv_transpose_direct',
+    },
+    recordIn(ctx, args) {
+      const [inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding, groups, outTensor] = args;
+      recordConv('aten.convolution.default', ctx, inTensor, weight, bias, stride, padding, dilation, transposed,
+        outputPadding, groups, outTensor);
+    },
+  };
+
+  // src/shaders/conv-with-clamp/index.ts:60-319: bias, then clamp, then narrow
+  const convWithClamp = {
+    name: 'et_vk.conv_with_clamp.default',
+    code: { all: 'the convolution kernels with the clamp epilogue enabled' },
+    recordIn(ctx, args) {
+      const [inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding, groups, outMin, outMax,
+        outTensor] = args;
+      recordConv('et_vk.conv_with_clamp.default', ctx, inTensor, weight, bias, stride, padding, dilation, transposed,
+        outputPadding, groups, outTensor, outMin === undefined ? undefined : outMin,
+        outMax === undefined ? undefined : outMax);
+    },
+  };
+
+  // ---------------------------------------------------------------- elementwise
+  function binary(name, isAdd, sign) {
+    return {
+      name,
+      code: { all: 'binary broadcast kernel' },
+      recordIn(ctx, args) {
+        const [in1, in2] = args;
+        const alpha = args.length === 4 ? args[2] : 1;
+        const out = args[args.length - 1];
+        if (!isFloatPair(in1) || in2.dtype !== in1.dtype || out.dtype !== in1.dtype) {
+          throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+        }
+        if (!broadcastable(in1, in2, out)) throw new Error(`${name}: Input shapes are not broadcastable to output shape`);
+        if (isAdd) native.recordAdd(ctx._h, in1._c(), in2._c(), alpha, sign < 0 ? 1 : 0, out._c());
+        else native.recordMul(ctx._h, in1._c(), in2._c(), out._c());
+      },
+    };
+  }
+  const add = binary('aten.add.Tensor', true, 1);
+  const sub = binary('aten.sub.Tensor', true, -1);
+  const mul = {
+    name: 'aten.mul.Tensor',
+    code: { all: 'binary broadcast kernel' },
+    recordIn(ctx, [in1, in2, out]) {
+      const name = 'aten.mul.Tensor';
+      if (!isFloatPair(in1) || in2.dtype !== in1.dtype || out.dtype !== in1.dtype) {
+        throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+      }
+      if (!broadcastable(in1, in2, out)) throw new Error(`${name}: Input shapes are not broadcastable to output shape`);
+      native.recordMul(ctx._h, in1._c(), in2._c(), out._c());
+    },
+  };
+
+  function unary(name, op) {
+    return {
+      name,
+      code: { all: 'unary kernel' },
+      recordIn(ctx, [inTensor, outTensor]) {
+        if (!isFloatPair(inTensor) || outTensor.dtype !== inTensor.dtype) {
+          throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+        }
+        if (inTensor.numel !== outTensor.numel) throw new Error(`${name}: input numel != output numel`);
+        native.recordUnary(ctx._h, op, inTensor._c(), outTensor._c());
+      },
+    };
+  }
+  const sigmoid = unary('aten.sigmoid.default', 0);
+  const relu = unary('aten.relu.default', 1);
+  const hardswish = unary('aten.hardswish.default', 2);
+
+  // ---------------------------------------------------------------- data movement
+  const cat = {
+    name: 'aten.cat.default',
+    code: { all: 'slab copy kernel per input' },
+    recordIn(ctx, [tensors, dim, out]) {
+      const name = 'aten.cat.default';
+      if (tensors.length === 0) throw new Error(`${name}: empty input list`);
+      const rank = out.shape.length;
+      const d = dim < 0 ? dim + rank : dim;
+      if (d < 0 || d >= rank) throw new Error(`${name}: dim out of range`);
+      let total = 0;
+      for (const t of tensors) {
+        if (t.dtype !== out.dtype || !isFloatPair(t)) throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+        if (t.shape.length !== rank) throw new Error(`${name}: input rank != output rank`);
+        for (let k = 0; k < rank; k++) {
+          if (k !== d && t.shape[k] !== out.shape[k]) throw new Error(`${name}: non-concat dim ${k} size mismatch`);
+        }
+        total += t.shape[d];
+      }
+      if (total !== out.shape[d]) throw new Error(`${name}: concat dim sizes do not sum to output`);
+      native.recordCat(ctx._h, tensors.map((t) => t._c()), d, out._c());
+    },
+  };
+
+  const splitWithSizesCopy = {
+    name: 'aten.split_with_sizes_copy.default',
+    code: { all: 'slab gather kernel per output' },
+    recordIn(ctx, [inTensor, splitSizes, dim, outs]) {
+      const name = 'aten.split_with_sizes_copy.default';
+      const rank = inTensor.shape.length;
+      const d = dim < 0 ? dim + rank : dim;
+      if (d < 0 || d >= rank) throw new Error(`${name}: dim out of range`);
+      if (outs.length !== splitSizes.length) throw new Error(`${name}: outputs (${outs.length}) != sizes (${splitSizes.length})`);
+      if (splitSizes.some((s) => s < 0)) throw new Error(`${name}: negative split size`);
+      if (splitSizes.reduce((a, b) => a + b, 0) !== inTensor.shape[d]) {
+        throw new Error(`${name}: sizes must sum to the split dim extent`);
+      }
+      outs.forEach((t, i) => {
+        if (t.dtype !== inTensor.dtype || !isFloatPair(t)) throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+        if (t.shape[d] !== splitSizes[i]) throw new Error(`${name}: output ${i} dim ${d} != split size`);
+      });
+      native.recordSplit(ctx._h, inTensor._c(), d, outs.map((t) => t._c()));
+    },
+  };
+
+  const upsampleNearest2d = {
+    name: 'aten.upsample_nearest2d.vec',
+    code: { all: 'nearest upsample kernel' },
+    recordIn(ctx, [inTensor, , , outTensor]) {
+      const name = 'aten.upsample_nearest2d.vec';
+      if (!isFloatPair(inTensor) || outTensor.dtype !== inTensor.dtype) {
+        throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+      }
+      if (inTensor.shape.length !== 4 || outTensor.shape.length !== 4) throw new Error(`${name}: input and output must be 4D NCHW`);
+      if (inTensor.shape[0] !== outTensor.shape[0] || inTensor.shape[1] !== outTensor.shape[1]) {
+        throw new Error(`${name}: output batch/channels must match input`);
+      }
+      if (outTensor.shape[2] < inTensor.shape[2] || outTensor.shape[3] < inTensor.shape[3]) {
+        throw new Error(`${name}: output spatial dims must be >= input spatial dims`);
+      }
+      native.recordUpsampleNearest2d(ctx._h, inTensor._c(), outTensor._c());
+    },
+  };
+
+  const maxPool2d = {
+    name: 'aten.max_pool2d_with_indices.default',
+    code: { all: 'max-pool kernel (values)' },
+    recordIn(ctx, [inTensor, kernelSize, stride, padding, dilation, ceilMode, outs]) {
+      const name = 'aten.max_pool2d_with_indices.default';
+      const k = parseHw(name, kernelSize, 'kernel_size');
+      const s = stride.length === 0 ? k : parseHw(name, stride, 'stride');
+      const p = parseHw(name, padding, 'padding');
+      const d = parseHw(name, dilation, 'dilation');
+      if (outs.length < 1) throw new Error(`${name}: expected 2 outputs [values, indices], got ${outs.length}`);
+      const vals = outs[0];
+      if (!isFloatPair(inTensor) || vals.dtype !== inTensor.dtype) {
+        throw new Error(`${name}: values tensors must have matching float32 or float16 dtype`);
+      }
+      if (inTensor.shape.length !== 4) throw new Error(`${name}: input must be 4D NCHW`);
+      if (ceilMode) throw new Error(`${name}: ceil_mode is not supported`);
+      native.recordMaxPool2d(ctx._h, inTensor._c(), k, s, p, d, vals._c());
+    },
+  };
+
+  function flatCopy(name) {
+    return {
+      name,
+      code: { all: 'device copy (elided when in and out alias)' },
+      recordIn(ctx, args) {
+        const src = args[0];
+        const out = args[args.length - 1];
+        if (src.byteLength !== out.byteLength) throw new Error(`${name}: input and output sizes differ`);
+        native.recordCopy(ctx._h, out.buffer.ptr, src.buffer.ptr, src.byteLength);
+      },
+    };
+  }
+
+  return {
+    add, sub, mul, sigmoid, relu, hardswish,
+    mm, addmm, linear, bmm,
+    convolution, convWithClamp, maxPool2d,
+    upsampleNearest2d,
+    cat, splitWithSizesCopy,
+    viewCopy: flatCopy('aten.view_copy.default'),
+    clone: flatCopy('aten.clone.default'),
+    squeezeCopy: flatCopy('aten.squeeze_copy.dims'),
+    unsqueezeCopy: flatCopy('aten.unsqueeze_copy.default'),
+    prepack: flatCopy('et_vk.prepack.default'),
+  };
+};

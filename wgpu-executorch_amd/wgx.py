@@ -67,7 +67,9 @@ _I = ctypes.c_int
 _U64 = ctypes.c_uint64
 SIGNATURES = {
     "wgx_ctx_create": (_I, [_I, ctypes.POINTER(_P)]),
+    "wgx_ctx_create_shared": (_I, [_P, ctypes.POINTER(_P)]),
     "wgx_ctx_destroy": (None, [_P]),
+    "wgx_free": (_I, [_P, _P]),
     "wgx_last_error": (ctypes.c_char_p, [_P]),
     "wgx_ctx_has_device": (_I, [_P]),
     "wgx_ctx_arch": (ctypes.c_char_p, [_P]),
@@ -164,13 +166,22 @@ class Tensor:
 class Context:
     """WgpuExecutionContext over one HIP device (device=-1: host-only validation)."""
 
-    def __init__(self, device: int = 0):
+    def __init__(self, device: int = 0, _parent: Optional["Context"] = None):
         h = ctypes.c_void_p()
-        r = lib().wgx_ctx_create(device, ctypes.byref(h))
+        if _parent is None:
+            r = lib().wgx_ctx_create(device, ctypes.byref(h))
+        else:
+            r = lib().wgx_ctx_create_shared(_parent.h, ctypes.byref(h))
         if r != 0:
             raise WgxError(r, f"wgx_ctx_create({device}) failed with status {r}")
         self.h = h
         self.destroyed = False
+
+    def shared(self) -> "Context":
+        """A further context on this context's device: same stream and buffer
+        registry, its own command list (several WgpuExecutionContexts over
+        one GPUDevice)."""
+        return Context(_parent=self)
 
     # ------------------------------------------------------------ plumbing
     def _check(self, r: int):
@@ -213,6 +224,10 @@ class Context:
         p = ctypes.c_void_p()
         self._check(lib().wgx_alloc(self.h, int(size), usage, ctypes.byref(p)))
         return p.value
+
+    def free(self, ptr: int):
+        """GPUBuffer.destroy(): later submits of commands that use it fail."""
+        self._check(lib().wgx_free(self.h, ptr))
 
     def buffer_size(self, ptr: int) -> int:
         off, size = ctypes.c_uint64(), ctypes.c_uint64()
