@@ -225,7 +225,7 @@ def cpu_baseline(I, budget_s=20.0):
             oracle.emu_conv2d(0, x, w, b, c["s"], c["p"])
         steps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 50:
+        if el >= budget_s or steps >= 10000:
             break
     flops = sum(conv_flops(c) for c in CONV2.values()) * steps
     return {"value": flops / el / 1e9, "unit": "GFLOP/s", "cores": n_thr, "kind": "port",
@@ -300,7 +300,7 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(I, budget_s=20.0)
+        cpu = cpu_baseline(I, budget_s=15.0)
 
     line = {
         "metric": "mm/conv GFLOP/s & % roofline; depthwise HBM GB/s; YOLO-N-shaped fp16 ms/frame",
