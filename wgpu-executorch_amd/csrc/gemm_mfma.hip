@@ -64,6 +64,8 @@ struct KParams {
   float cmin, cmax;
   ConvGeom g;
   int tiles_n;
+  int gm;            // m-tiles per group of the tile order
+  uint32_t b_bytes;  // B_CONV: bytes of one input image
   int batch;
 };
 
@@ -97,6 +99,30 @@ __device__ __forceinline__ uint16_t st_bits(float v) {
 
 __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
 
+// Buffer descriptors for raw buffer loads (word 3 = 0x00020000: the gfx9
+// raw-buffer format).  An offset at or past the range reads as zero.
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr uint32_t OOB = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld_b128(rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t ld_b16(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void st_b128(uint4 v, rsrc_t r, uint32_t off) {
+  using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+  const u32x4 d = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(d, r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void st_b16(uint32_t v, rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b16((unsigned short)v, r, (int)off, 0, 0);
+}
+
 // One persistent block walks tiles blockIdx', blockIdx'+G, ... (G = grid size;
 // blockIdx' is the XCD-aware renumbering).  Per tile: K slices of BK = 64 go
 // through two LDS stages, the global loads of slice t+1 are in flight while
@@ -110,23 +136,24 @@ __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return lo 
 // writes before the coalesced 16-byte global stores.
 template <int BM, int BN, int WGM, int WGN, int BMODE, bool AVEC, bool BVEC, bool BF>
 __global__ __launch_bounds__(WGM * WGN * 64)
-__attribute__((amdgpu_waves_per_eu(BM * BN <= 64 * 64 ? 4 : 2))) void k_gemm(KParams p) {
+__attribute__((amdgpu_waves_per_eu(2))) void k_gemm(KParams p) {
   extern __shared__ uint4 smem_u4[];
   uint16_t* smem = reinterpret_cast<uint16_t*>(smem_u4);
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = (BM + BN) * RS;
+  constexpr int BMAX = BM > BN ? BM : BN;  // bias floats parked in LDS
   constexpr int CA = BM * BK / 8 / NT;  // 16-byte A chunks per thread
   constexpr int CBV = BN * BK / 8 / NT; // 16-byte B chunks per thread (B_NK)
   constexpr int KR = BK * BN / NT;      // k run per lane (column loaders)
   constexpr bool KNV = BMODE == B_KN && BVEC;  // 4x8 block transpose loader
-  constexpr int NKB = KNV ? 2 * BN / NT : 1;   // 4x8 blocks per thread
+  constexpr int NKB = KNV ? (2 * BN + NT - 1) / NT : 1;  // 4x8 blocks per thread
   constexpr int RBV = BMODE == B_NK ? CBV : (KNV ? 4 * NKB : 1);
   constexpr int RBS = (BMODE == B_NK || KNV) ? 1 : KR / 2;
   static_assert(TM >= 1 && TN >= 1 && CA >= 1 && (BMODE != B_NK || CBV >= 1), "tile too small");
   static_assert(BMODE == B_NK || KNV || (BN >= 64 && KR % 8 == 0), "column loader needs BN >= 64");
-  static_assert(!KNV || (2 * BN) % NT == 0, "4x8 block loader needs 2*BN divisible by threads");
+  static_assert(!KNV || (2 * BN) % 64 == 0, "4x8 block loader keeps whole waves busy or idle");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -146,19 +173,50 @@ __attribute__((amdgpu_waves_per_eu(BM * BN <= 64 * 64 ? 4 : 2))) void k_gemm(KPa
   // ------------------------------------------------ per-tile load state
   const int nl = tid % BN;    // column loaders: this lane's column in the tile
   const int krun = tid / BN;  // wave-uniform since BN >= 64
+  // Operands are read with raw buffer loads.  Each tile gets buffer
+  // descriptors whose range ends where the operand's valid data ends, and a
+  // masked element (k or n past the edge, an out-of-image tap) is given the
+  // offset OOB, which the hardware range check turns into a zero.  So every
+  // load is unconditional and branch-free, and the loads of a slice are all
+  // in flight together.
   struct LoadState {
-    const uint16_t* A;
-    const uint16_t* B;
-    int m0, n0, gn_col, colbase;
+    rsrc_t ra, rb;
+    int m0, n0, z, gn_col, colbase;
     unsigned long long cmask;
+    uint32_t bias_h;  // this thread's bias element of the tile (raw bits)
   };
   auto tile_state = [&](int tile) {
     LoadState s;
+    // grouped order: p.gm m-tiles walked first, then n, so a run of
+    // consecutive tiles (one XCD's share) covers a compact rectangle
     const int z = tile / tiles_mn, r = tile % tiles_mn;
-    s.m0 = (r / p.tiles_n) * BM;
-    s.n0 = (r % p.tiles_n) * BN;
-    s.A = p.A + (long long)z * p.sA;
-    s.B = p.B + (long long)z * p.sB;
+    const int gsz = p.gm * p.tiles_n;
+    const int grp = r / gsz, rr = r - grp * gsz;
+    const int gmh = min(p.gm, tiles_m - grp * p.gm);
+    s.m0 = (grp * p.gm + rr % gmh) * BM;
+    s.n0 = (rr / gmh) * BN;
+    s.z = z;
+    const int mrows = min(BM, M - s.m0);
+    s.ra = make_rsrc(p.A + (long long)z * p.sA + (long long)s.m0 * p.lda,
+                     (uint32_t)((mrows - 1) * p.lda + K) * 2u);
+    if constexpr (BMODE == B_NK) {
+      const int nrows = min(BN, N - s.n0);
+      s.rb = make_rsrc(p.B + (long long)z * p.sB + (long long)s.n0 * p.ldb,
+                       (uint32_t)((nrows - 1) * p.ldb + K) * 2u);
+    } else if constexpr (BMODE == B_CONV) {
+      s.rb = make_rsrc(p.B + (long long)z * p.sB, p.b_bytes);
+    } else {
+      s.rb = make_rsrc(p.B, 0u);  // B_KN: rebuilt per slice (see load_slice)
+    }
+    // bias: thread t < BN (per column) or < BM (per row) fetches element t
+    // of the tile; it is parked in LDS when the tile starts
+    s.bias_h = 0u;
+    if (p.bias_mode != BIAS_NONE) {
+      const bool col = p.bias_mode == BIAS_COL;
+      const int lim = col ? N : M, b0 = col ? s.n0 : s.m0, cnt = col ? BN : BM;
+      const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)lim * 2u);
+      s.bias_h = ld_b16(rbias, (tid < cnt && b0 + tid < lim) ? (uint32_t)(b0 + tid) * 2u : OOB);
+    }
     s.gn_col = s.n0 + nl;
     s.colbase = 0;
     s.cmask = 0ull;
@@ -189,76 +247,72 @@ __attribute__((amdgpu_waves_per_eu(BM * BN <= 64 * 64 ? 4 : 2))) void k_gemm(KPa
   };
   Regs R0;
 
-  // Every global load below is unconditional and reads an in-bounds address
-  // (out-of-range rows / k are clamped, out-of-image taps read element 0);
-  // the value is zeroed afterwards with a select, so all of a slice's loads
-  // are in flight at once instead of each waiting behind the previous one.
-  auto load_rows = [&](const uint16_t* __restrict__ src, long long ld, int r0, int rlim,
-                       int k0, auto vec_tag, uint4* dst, int nchunk) {
+  // k-contiguous rows (A, and B in the B_NK form): 8 lanes cover one row's
+  // 64 k of the slice; rows past the tile's valid rows fall outside the
+  // descriptor's range.
+  auto load_rows = [&](rsrc_t rs, long long ld, int k0, auto vec_tag, uint4* dst, int nchunk) {
     constexpr bool VEC = decltype(vec_tag)::value;
 #pragma unroll
     for (int i = 0; i < nchunk; ++i) {
       const int c = tid + i * NT;
       const int row = c >> 3, kc = c & 7;
-      const int gr = r0 + row, gk = k0 + kc * 8;
-      const int grc = gr < rlim ? gr : rlim - 1;
+      const int gk = k0 + kc * 8;
+      const uint32_t base = (uint32_t)(row * ld + gk) * 2u;
       if constexpr (VEC) {
-        const bool ok = gr < rlim && gk < K;
-        const uint4 v = *reinterpret_cast<const uint4*>(src + (long long)grc * ld + (ok ? gk : 0));
-        dst[i] = ok ? v : make_uint4(0, 0, 0, 0);
+        dst[i] = ld_b128(rs, gk < K ? base : OOB);
       } else {
         uint32_t h[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const bool ok = gr < rlim && gk + e < K;
-          const uint32_t v = src[(long long)grc * ld + (ok ? gk + e : 0)];
-          h[e] = ok ? v : 0u;
-        }
+        for (int e = 0; e < 8; ++e) h[e] = ld_b16(rs, gk + e < K ? base + 2u * e : OOB);
         dst[i] = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]),
                             pack2(h[6], h[7]));
       }
     }
   };
 
-  const uint32_t* ktab_lds = reinterpret_cast<const uint32_t*>(smem + 2 * STAGE);
+  float* bias_lds = reinterpret_cast<float*>(smem + 2 * STAGE);
+  const uint32_t* ktab_lds = reinterpret_cast<const uint32_t*>(smem + 2 * STAGE + 2 * BMAX);
   auto load_slice = [&](const LoadState& st, int k0, Regs& R) {
-    load_rows(st.A, p.lda, st.m0, M, k0, std::integral_constant<bool, AVEC>{}, R.a, CA);
+    load_rows(st.ra, p.lda, k0, std::integral_constant<bool, AVEC>{}, R.a, CA);
     if constexpr (BMODE == B_NK) {
-      load_rows(st.B, p.ldb, st.n0, N, k0, std::integral_constant<bool, BVEC>{}, R.bv, CBV);
-    } else if constexpr (KNV) {
-      // 4 k-rows x 8 columns per block, four 16-byte loads
-#pragma unroll
-      for (int i = 0; i < NKB; ++i) {
-        const int c = tid + i * NT;
-        const int kg = c & 15, ng = c >> 4;
-        const int gn = st.n0 + ng * 8;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int gk = k0 + kg * 4 + j;
-          const bool ok = gk < K && gn < N;
-          const uint4 v = *reinterpret_cast<const uint4*>(
-              st.B + (long long)(gk < K ? gk : K - 1) * p.ldb + (ok ? gn : 0));
-          R.bv[4 * i + j] = ok ? v : make_uint4(0, 0, 0, 0);
-        }
-      }
+      load_rows(st.rb, p.ldb, k0, std::integral_constant<bool, BVEC>{}, R.bv, CBV);
     } else if constexpr (BMODE == B_KN) {
-      const int kb = k0 + krun * KR;
-      const int gnc = st.gn_col < N ? st.gn_col : N - 1;
-      uint32_t v[KR];
+      // rows of n: the descriptor starts at (k0, n0) and ends after the last
+      // valid element of the slice's last valid row
+      const int krows = min(BK, K - k0);  // <= 0 past K: every load reads zero
+      const int kb0 = krows > 0 ? k0 : 0;
+      const rsrc_t rs = make_rsrc(p.B + (long long)st.z * p.sB + (long long)kb0 * p.ldb + st.n0,
+                                  krows > 0 ? (uint32_t)((krows - 1) * p.ldb + (N - st.n0)) * 2u : 0u);
+      if constexpr (KNV) {
+        // 4 k-rows x 8 columns per block, four 16-byte loads
 #pragma unroll
-      for (int e = 0; e < KR; ++e) {
-        const int kk = kb + e < K ? kb + e : K - 1;
-        v[e] = st.B[(long long)kk * p.ldb + gnc];
-      }
+        for (int i = 0; i < NKB; ++i) {
+          const int c = tid + i * NT;
+          if (2 * BN % NT != 0 && c >= 2 * BN) break;  // wave-uniform
+          const int kg = c & 15, ng = c >> 4;
+          const bool nok = st.n0 + ng * 8 < N;
 #pragma unroll
-      for (int e = 0; e < KR; e += 2) {
-        const uint32_t lo = (st.gn_col < N && kb + e < K) ? v[e] : 0u;
-        const uint32_t hi = (st.gn_col < N && kb + e + 1 < K) ? v[e + 1] : 0u;
-        R.bs[e / 2] = pack2(lo, hi);
+          for (int j = 0; j < 4; ++j) {
+            const int kr = kg * 4 + j;
+            R.bv[4 * i + j] = ld_b128(rs, (nok && kr < krows) ? (uint32_t)(kr * p.ldb + ng * 8) * 2u : OOB);
+          }
+        }
+      } else {
+        const int kb = krun * KR;
+        const bool nok = st.gn_col < N;
+        uint32_t v[KR];
+#pragma unroll
+        for (int e = 0; e < KR; ++e)
+          v[e] = ld_b16(rs, (nok && kb + e < krows) ? (uint32_t)((kb + e) * p.ldb + nl) * 2u : OOB);
+#pragma unroll
+        for (int e = 0; e < KR; e += 2) R.bs[e / 2] = pack2(v[e], v[e + 1]);
       }
     } else {
-      // im2col: per-k entries (offset << 6) | tap, staged in LDS
-      const uint32_t* tl = ktab_lds + k0 + krun * KR;
+      // im2col: per-k entries (offset << 6) | tap, staged in LDS; a slice
+      // past K reads the first table rows and masks every tap
+      const bool live = k0 < K;
+      const unsigned long long lmask = live ? st.cmask : 0ull;
+      const uint32_t* tl = ktab_lds + (live ? k0 : 0) + krun * KR;
       uint32_t ent[KR];
 #pragma unroll
       for (int q = 0; q < KR; q += 4) {
@@ -271,15 +325,11 @@ __attribute__((amdgpu_waves_per_eu(BM * BN <= 64 * 64 ? 4 : 2))) void k_gemm(KPa
       uint32_t v[KR];
 #pragma unroll
       for (int e = 0; e < KR; ++e) {
-        const bool ok = (st.cmask >> (ent[e] & 63u)) & 1ull;
-        v[e] = st.B[ok ? st.colbase + (int)(ent[e] >> 6) : 0];
+        const bool ok = (lmask >> (ent[e] & 63u)) & 1ull;
+        v[e] = ld_b16(st.rb, ok ? (uint32_t)(st.colbase + (int)(ent[e] >> 6)) * 2u : OOB);
       }
 #pragma unroll
-      for (int e = 0; e < KR; e += 2) {
-        const uint32_t lo = ((st.cmask >> (ent[e] & 63u)) & 1ull) ? v[e] : 0u;
-        const uint32_t hi = ((st.cmask >> (ent[e + 1] & 63u)) & 1ull) ? v[e + 1] : 0u;
-        R.bs[e / 2] = pack2(lo, hi);
-      }
+      for (int e = 0; e < KR; e += 2) R.bs[e / 2] = pack2(v[e], v[e + 1]);
     }
   };
 
@@ -302,6 +352,7 @@ __attribute__((amdgpu_waves_per_eu(BM * BN <= 64 * 64 ? 4 : 2))) void k_gemm(KPa
 #pragma unroll
       for (int i = 0; i < NKB; ++i) {
         const int c = tid + i * NT;
+        if (2 * BN % NT != 0 && c >= 2 * BN) break;  // wave-uniform
         const int kg = c & 15, ng = c >> 4;
         const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 0]);
         const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 1]);
@@ -352,44 +403,71 @@ __attribute__((amdgpu_waves_per_eu(BM * BN <= 64 * 64 ? 4 : 2))) void k_gemm(KPa
   };
 
   if constexpr (BMODE == B_CONV) {
-    uint32_t* tw = reinterpret_cast<uint32_t*>(smem + 2 * STAGE);
+    uint32_t* tw = reinterpret_cast<uint32_t*>(smem + 2 * STAGE + 2 * BMAX);
     for (int i = tid; i < KT * BK; i += NT) tw[i] = p.ktab[i];
     __syncthreads();
   }
 
+  // Slice s of a tile lives in register set R[s % 2] between its global
+  // load and its LDS store: the loads run two K slices ahead of the MFMAs.
+  Regs R1;
   int tile = rb;
   if (tile >= ntiles) return;
   LoadState cur = tile_state(tile);
   load_slice(cur, 0, R0);
+  load_slice(cur, BK, R1);
 
   constexpr int CS = BN + 8;
   static_assert(BM * CS <= 2 * STAGE, "C staging must fit in the A/B buffers");
 
+  // One K step: slice t+1 (held in Rn) goes to LDS, slice t+3 is requested
+  // into the freed registers, slice t is multiplied.  The stage written here
+  // was last read in step t-1, which ended with a barrier.  Nothing in a
+  // step is conditional: a slice at or past K loads as zeros (its offsets are
+  // out of range), so the compiler can count outstanding loads exactly and
+  // wait only for the slice being stored.
+  auto step = [&](int t, Regs& Rn) {
+    store_slice((t + 1) & 1, Rn);
+    load_slice(cur, (t + 3) * BK, Rn);
+    compute_slice(t & 1);
+    __syncthreads();
+  };
+
   while (true) {
     __syncthreads();  // the previous tile's epilogue is done with LDS
     store_slice(0, R0);
-    __syncthreads();
+    if (p.bias_mode != BIAS_NONE && tid < BMAX) bias_lds[tid] = p.beta * ld_f32<BF>((uint16_t)cur.bias_h);
+    load_slice(cur, 2 * BK, R0);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    __syncthreads();
 
-    for (int t = 0; t < KT; ++t) {
-      if (t + 1 < KT) load_slice(cur, (t + 1) * BK, R0);
-      compute_slice(t & 1);
-      if (t + 1 < KT) store_slice((t + 1) & 1, R0);
-      __syncthreads();
+    // slice s is held in R[s % 2]
+    if (KT & 1) {
+      step(0, R1);
+      for (int t = 1; t < KT; t += 2) {
+        step(t, R0);
+        step(t + 1, R1);
+      }
+    } else {
+      for (int t = 0; t < KT; t += 2) {
+        step(t, R1);
+        step(t + 1, R0);
+      }
     }
 
-    // the next tile's first slice goes out before this tile's epilogue
+    // the next tile's first two slices go out before this tile's epilogue
     const int m0 = cur.m0, n0 = cur.n0;
     const int z = tile / tiles_mn;
     const int next = tile + G;
     if (next < ntiles) {
       cur = tile_state(next);
       load_slice(cur, 0, R0);
+      load_slice(cur, BK, R1);
     }
 
     // ------------------------------------------------ epilogue via LDS
@@ -399,22 +477,19 @@ __attribute__((amdgpu_waves_per_eu(BM * BN <= 64 * 64 ? 4 : 2))) void k_gemm(KPa
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int row = wm * WM + i * 32 + frow;
-      const int gm = m0 + row;
-      float rowb = 0.0f;
-      if (p.bias_mode == BIAS_ROW && gm < M) rowb = p.beta * ld_f32<BF>(p.bias[gm]);
+      const float rowb = p.bias_mode == BIAS_ROW ? bias_lds[row] : 0.0f;
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int col = wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+          float4 bc = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (p.bias_mode == BIAS_COL) bc = *reinterpret_cast<const float4*>(bias_lds + col);
+          const float bb[4] = {bc.x, bc.y, bc.z, bc.w};
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            float x = p.alpha * acc[i][j][4 * g + e] + rowb;
-            if (p.bias_mode == BIAS_COL) {
-              const int gn = n0 + col + e;
-              if (gn < N) x += p.beta * ld_f32<BF>(p.bias[gn]);
-            }
+            float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
             if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
             v[e] = x;
           }
@@ -425,23 +500,28 @@ __attribute__((amdgpu_waves_per_eu(BM * BN <= 64 * 64 ? 4 : 2))) void k_gemm(KPa
     }
     __syncthreads();
 
-    uint16_t* __restrict__ C = p.C + (long long)z * p.sC;
+    // Stores through a descriptor whose range ends after the tile's last valid
+    // row; columns past N get the offset OOB, which the hardware drops.
+    const int mrows = min(BM, M - m0);
+    const rsrc_t rc = make_rsrc(p.C + (long long)z * p.sC + (long long)m0 * p.ldc + n0,
+                                (uint32_t)((mrows - 1) * p.ldc + (N - n0)) * 2u);
     const bool cvec = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0) &&
-                      ((p.sC & 7) == 0);
+                      ((p.sC & 7) == 0) && ((N & 7) == 0);
     constexpr int CC = BM * BN / 8 / NT;
 #pragma unroll
     for (int i = 0; i < CC; ++i) {
       const int c = tid + i * NT;
       const int row = c / (BN / 8), cc = c % (BN / 8);
-      const int gm = m0 + row, gn = n0 + cc * 8;
-      if (gm >= M) continue;
-      const uint16_t* srow = cs + row * CS + cc * 8;
-      if (cvec && gn + 8 <= N) {
-        *reinterpret_cast<uint4*>(C + (long long)gm * p.ldc + gn) = *reinterpret_cast<const uint4*>(srow);
+      const uint4 cv = *reinterpret_cast<const uint4*>(cs + row * CS + cc * 8);
+      const int gn = n0 + cc * 8;
+      const uint32_t off = (uint32_t)(row * p.ldc + cc * 8) * 2u;
+      if (cvec) {
+        st_b128(cv, rc, gn < N ? off : OOB);
       } else {
+        const uint32_t w[4] = {cv.x, cv.y, cv.z, cv.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (gn + e < N) C[(long long)gm * p.ldc + gn + e] = srow[e];
+          st_b16((w[e >> 1] >> (16 * (e & 1))) & 0xffffu, rc, gn + e < N ? off + 2u * e : OOB);
       }
     }
     if (next >= ntiles) break;
@@ -464,8 +544,8 @@ template <int BM, int BN, int WGM, int WGN, int BMODE, bool AVEC, bool BVEC, boo
 hipError_t launch_one(const KParams& kp, int batch, hipStream_t s) {
   auto fn = k_gemm<BM, BN, WGM, WGN, BMODE, AVEC, BVEC, BF>;
   const size_t stages = (size_t)2 * (BM + BN) * RS * sizeof(uint16_t);
-  const size_t lds =
-      stages + (BMODE == B_CONV ? (size_t)conv_ktab_rows(kp.K) * sizeof(uint32_t) : 0);
+  const size_t lds = stages + (size_t)(BM > BN ? BM : BN) * sizeof(float) +
+                     (BMODE == B_CONV ? (size_t)conv_ktab_rows(kp.K) * sizeof(uint32_t) : 0);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   static bool attr_set = false;
   if (!attr_set && s != name_only()) {
@@ -485,6 +565,14 @@ hipError_t launch_one(const KParams& kp, int batch, hipStream_t s) {
   if (grid > ntiles) grid = ntiles;
   KParams k2 = kp;
   k2.batch = batch;
+  // group height: one XCD's share of a round (grid/8 tiles) as a rectangle
+  // that is about square in elements
+  {
+    const int tiles_m = (kp.M + BM - 1) / BM;
+    const double per_xcd = (double)(grid < 8 ? 1 : grid / 8);
+    int gm = (int)lround(sqrt(per_xcd * BN / BM));
+    k2.gm = gm < 1 ? 1 : (gm > tiles_m ? tiles_m : gm);
+  }
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WGM * WGN * 64), lds, s, k2);
   return hipGetLastError();
 }
@@ -497,7 +585,8 @@ constexpr Tile kTiles[] = {{256, 128, 4, 2}, {128, 256, 2, 4}, {128, 128, 2, 2},
                            {64, 64, 2, 2}};
 
 size_t tile_lds(const Tile& t, int bmode, int K) {
-  return (size_t)2 * (t.bm + t.bn) * RS * 2 + (bmode == B_CONV ? (size_t)conv_ktab_rows(K) * 4 : 0);
+  return (size_t)2 * (t.bm + t.bn) * RS * 2 + (size_t)(t.bm > t.bn ? t.bm : t.bn) * 4 +
+         (bmode == B_CONV ? (size_t)conv_ktab_rows(K) * 4 : 0);
 }
 
 // Picks the block tile: fewest rounds over the 256 CUs (a block of 8 waves
@@ -531,13 +620,11 @@ Tile choose_tile(int M, int N, int K, int batch, bool avec, int bmode) {
 
 template <int BMODE, bool AVEC, bool BVEC, bool BF>
 hipError_t dispatch_tile(const Tile& t, const KParams& kp, int batch, hipStream_t s) {
-  // the 4x8 KN block loader needs 2*BN divisible by the thread count
-  constexpr bool KN = BMODE == B_KN;
-  if (t.bm == 256 && t.bn == 128) return launch_one<256, 128, 4, 2, BMODE, AVEC, (KN ? false : BVEC), BF>(kp, batch, s);
+  if (t.bm == 256 && t.bn == 128) return launch_one<256, 128, 4, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
   if (t.bm == 128 && t.bn == 256) return launch_one<128, 256, 2, 4, BMODE, AVEC, BVEC, BF>(kp, batch, s);
   if (t.bm == 128 && t.bn == 128) return launch_one<128, 128, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
-  if (t.bm == 128 && t.bn == 64) return launch_one<128, 64, 2, 2, BMODE, AVEC, (KN ? false : BVEC), BF>(kp, batch, s);
-  return launch_one<64, 64, 2, 2, BMODE, AVEC, (KN ? false : BVEC), BF>(kp, batch, s);
+  if (t.bm == 128 && t.bn == 64) return launch_one<128, 64, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
+  return launch_one<64, 64, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
 }
 
 }  // namespace
@@ -565,6 +652,16 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
   kp.cmin = d.cmin;
   kp.cmax = d.cmax;
   kp.g = d.g;
+  kp.gm = 1;
+  kp.b_bytes = 0;
+  // buffer offsets are 31-bit: a tile's rows of A / B, a slice's rows of a
+  // [K,N] operand and one im2col input image must stay below 2 GiB
+  if (d.lda >= (1LL << 22) || d.ldb >= (1LL << 22)) return hipErrorInvalidValue;
+  if (d.bmode == B_CONV) {
+    const long long img = (long long)d.K / (d.g.KH * d.g.KW) * d.g.IH * d.g.IW * 2;
+    if (img >= (1LL << 31)) return hipErrorInvalidValue;
+    kp.b_bytes = (uint32_t)img;
+  }
   const bool bf = d.dtype == WGX_BFLOAT16;
   const auto aligned16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   const bool avec = (d.K % 8 == 0) && (d.lda % 8 == 0) && (d.sA % 8 == 0) && aligned16(d.A);
@@ -577,9 +674,9 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
     bvec = false;
   Tile t = choose_tile(d.M, d.N, d.K, d.batch, avec, d.bmode);
   if (d.bmode == B_NK && !bvec) t = {64, 64, 2, 2};
-  if (d.bmode == B_KN && !bvec && !(t.bm == 128 && t.bn == 128)) t = {64, 64, 2, 2};
+  if (d.bmode == B_KN && !bvec) t = {64, 64, 2, 2};
   kp.tiles_n = (d.N + t.bn - 1) / t.bn;
-  const bool knv = d.bmode == B_KN && bvec && (2 * t.bn) % (t.wgm * t.wgn * 64) == 0;
+  const bool knv = d.bmode == B_KN && bvec;
   if (name) {
     char buf[96];
     static const char* modes[] = {"nk", "kn", "conv"};
@@ -607,13 +704,9 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
               : dispatch_tile<B_NK, true, true, false>(t, kp, d.batch, s);
   }
   if (d.bmode == B_KN) {
-    if (!bvec) {
-      if (t.bm == 128)
-        return bf ? launch_one<128, 128, 2, 2, B_KN, true, false, true>(kp, d.batch, s)
-                  : launch_one<128, 128, 2, 2, B_KN, true, false, false>(kp, d.batch, s);
+    if (!bvec)
       return bf ? launch_one<64, 64, 2, 2, B_KN, true, false, true>(kp, d.batch, s)
                 : launch_one<64, 64, 2, 2, B_KN, true, false, false>(kp, d.batch, s);
-    }
     return bf ? dispatch_tile<B_KN, true, true, true>(t, kp, d.batch, s)
               : dispatch_tile<B_KN, true, true, false>(t, kp, d.batch, s);
   }
