@@ -204,7 +204,47 @@ def detail_configs(W, I, quick=False):
     nb = (2 * 16 * 1024 * 64 + 16 * 1024 * 1024) * 2
     k, s, a = measure(W, b_bmm, max(4, int(9 * scale)), reps_shape=20, reps_amort=3)
     rec("4_bmm_f16", k, s, a, 2.0 * 16 * 1024 * 1024 * 64, nb, "hbm", None)
+
+    # config 5: the YOLO-N-style fp16 program through Node recordProgram
+    y = yolo_frame(quick)
+    if y is not None:
+        out["5_yolo_n_f16"] = y
+        log(f"{'5_yolo_n_f16':28s} {y['ops']} ops / {y['commands']} commands      "
+            f"frame {y['frame_ms_wall']*1e3:9.1f} us wall (submit+sync), {y['frame_ms_device']*1e3:9.1f} us device  "
+            f"{y['conv_GFLOPs_device']:8.1f} conv GFLOP/s")
     return out
+
+
+def yolo_frame(quick=False):
+    """ms/frame of the synthetic YOLO-N-style fp16 program, input [1,3,640,640]:
+    recorded once with WgpuExecutionContext.recordProgram in Node, one
+    submit()+sync() per frame (median wall time) and device time per submit."""
+    import importlib
+    import shutil
+    import subprocess
+    import tempfile
+
+    node = shutil.which("node")
+    if node is None:
+        log("5_yolo_n_f16: node is not installed, skipped")
+        return None
+    Y = importlib.import_module("wgpu_executorch_amd.yolo_program")
+    d = tempfile.mkdtemp(prefix="wgx_yolo_")
+    try:
+        info = Y.write(d, img=640)
+        runner = os.path.join(ROOT, "wgpu-executorch_amd", "js", "run_program.js")
+        reps = 20 if quick else 100
+        r = subprocess.run([node, runner, d, "--device", "0", "--warmup", "5", "--reps", str(reps)],
+                           capture_output=True, text=True, timeout=300)
+        if r.returncode != 0:
+            raise RuntimeError("run_program.js failed: " + r.stderr[-2000:])
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    res.update({"params": info["params"], "conv_gflop": info["conv_flops"] / 1e9,
+                "conv_GFLOPs_device": info["conv_flops"] / res["frame_ms_device"] / 1e6,
+                "unit": "ms/frame"})
+    return res
 
 
 # ---------------------------------------------------------------- CPU baseline

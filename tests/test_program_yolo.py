@@ -1,0 +1,214 @@
+"""The YOLO-N-style fp16 program (recordProgram end to end).
+
+CPU: the generator emits a valid program in the reference's format (pool
+rule, lifetimes, alignment, sizes); the JS host layer records it on a
+host-only device (every driver's validation runs); the program evaluator the
+GPU runs are checked against is pinned against torch on each operator and
+against the reference's own program KAT.
+GPU: the program runs through Node -> N-API -> libwgx on GPU 0 and its output
+is compared with the CPU evaluation of the same program, at 160x160 and at
+the full 640x640 configuration.
+"""
+import importlib
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+RUNNER = os.path.join(ROOT, "wgpu-executorch_amd", "js", "run_program.js")
+NODE = shutil.which("node")
+needs_node = pytest.mark.skipif(NODE is None, reason="node is not installed")
+
+
+@pytest.fixture(scope="module")
+def Y(pkg):
+    return importlib.import_module("wgpu_executorch_amd.yolo_program")
+
+
+def _tensor_ids(prog, arg):
+    v = prog["values"][arg]
+    if v["type"] == "tensor":
+        return [arg]
+    if v["type"] == "tensorlist":
+        return list(v["items"])
+    return []
+
+
+def test_generator_matches_the_configuration(Y):
+    prog, weights, info = Y.build()
+    assert info["input_shape"] == [1, 3, 640, 640]
+    assert info["output_shape"] == [1, 84, 8400]  # three heads: 6400 + 1600 + 400 anchors
+    assert 2.2e6 <= info["params"] <= 2.8e6      # "about 2.5M parameters"
+    names = {op["name"] for op in prog["chain"]}
+    assert {"aten.convolution.default", "aten.sigmoid.default", "aten.mul.Tensor", "aten.cat.default",
+            "aten.upsample_nearest2d.vec", "aten.split_with_sizes_copy.default"} <= names
+    convs = [op for op in prog["chain"] if op["name"] == "aten.convolution.default"]
+    groups = [prog["values"][op["args"][8]]["value"] for op in convs]
+    assert any(g > 1 for g in groups)  # depthwise blocks present
+    # channel progression 16/32/64/128/256 at strides 2..32
+    outs = [prog["values"][op["args"][-1]]["shape"] for op in convs]
+    seen = {(s[1], 640 // s[2]) for s in outs}
+    for c, s in [(16, 2), (32, 4), (64, 8), (128, 16), (256, 32)]:
+        assert (c, s) in seen
+
+
+def test_generator_pool_plan_follows_converter_rule(Y):
+    prog, weights, _ = Y.build(img=160)
+    vals = prog["values"]
+    es = {"float16": 2, "float32": 4, "int32": 4}
+    sizes = {}
+    for v in vals:
+        if v["type"] == "tensor" and "memObjId" in v:
+            nb = int(np.prod(v["shape"])) * es[v["dtype"]]
+            sizes[v["memObjId"]] = max(sizes.get(v["memObjId"], 0), nb)
+    # utils/pte_to_program.py:386-413: pool size = largest tensor in the pool
+    assert {p["id"]: p["size"] for p in prog["memoryPlan"]["pools"]} == sizes
+    # constants: 4-byte aligned inside weights.bin, as the fp16 converter writes them
+    for v in vals:
+        if v["type"] == "tensor" and "weightsOffset" in v:
+            assert "memObjId" not in v and v["weightsOffset"] % 4 == 0
+            assert v["weightsOffset"] + v["weightsLength"] <= len(weights)
+    # no op reads a pool another live tensor occupies: check lifetimes per pool
+    first, last = {}, {}
+    for k, op in enumerate(prog["chain"]):
+        for a in op["args"]:
+            for t in _tensor_ids(prog, a):
+                if "memObjId" in vals[t]:
+                    first.setdefault(t, k)
+                    last[t] = k
+    for t in prog["inputIds"]:
+        first[t] = -1
+    for t in prog["outputIds"]:
+        last[t] = len(prog["chain"])
+    by_pool = {}
+    for t in first:
+        by_pool.setdefault(vals[t]["memObjId"], []).append((first[t], last[t]))
+    for spans in by_pool.values():
+        spans.sort()
+        for (s0, e0), (s1, e1) in zip(spans, spans[1:]):
+            assert e0 < s1, "two live tensors share a pool"
+
+
+@needs_node
+def test_js_host_records_the_program(Y, tmp_path):
+    Y.write(str(tmp_path), img=160)
+    r = subprocess.run([NODE, RUNNER, str(tmp_path), "--device", "-1", "--record-only"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    prog = json.load(open(tmp_path / "program.json"))
+    assert res["ops"] == len(prog["chain"]) and res["commands"] >= len(prog["chain"])
+
+
+# ------------------------------------------------------------ evaluator pins
+def test_evaluator_reference_program_kat(orc):
+    """The reference's 2-op add+mm program KAT (tests/api/program.test.ts:54-68)."""
+    from oracle import program_eval
+
+    prog = {"version": "1",
+            "chain": [{"name": "aten.add.Tensor", "args": [0, 1, 2, 3]},
+                      {"name": "aten.mm.default", "args": [3, 4, 5]}],
+            "values": [{"type": "tensor", "shape": [2, 2], "dtype": "float32", "memObjId": 0},
+                       {"type": "tensor", "shape": [2, 2], "dtype": "float32", "memObjId": 1},
+                       {"type": "scalar", "value": 1.5},
+                       {"type": "tensor", "shape": [2, 2], "dtype": "float32", "memObjId": 2},
+                       {"type": "tensor", "shape": [2, 2], "dtype": "float32", "memObjId": 3},
+                       {"type": "tensor", "shape": [2, 2], "dtype": "float32", "memObjId": 0}],
+            "inputIds": [0, 1, 4], "outputIds": [5],
+            "memoryPlan": {"pools": [{"id": i, "size": 16} for i in range(4)]}}
+    ins = [np.array([1, 2, 3, 4.0]), np.array([10, 20, 30, 40.0]), np.array([1, 2, 3, 4.0])]
+    out = program_eval.evaluate(prog, b"", ins)[0]
+    assert out.ravel().tolist() == [112, 160, 240, 352]
+
+
+def test_evaluator_ops_match_torch(orc):
+    """Each non-conv operator of the evaluator against torch on the CPU."""
+    import torch
+    import torch.nn.functional as F
+
+    from oracle import program_eval
+
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((1, 6, 9, 7)).astype(np.float16).astype(np.float64)
+
+    def run(name, args_vals, out_shapes, out_dtype="float16"):
+        values, args = [], []
+        for a in args_vals:
+            if isinstance(a, np.ndarray):
+                values.append({"type": "tensor", "shape": list(a.shape), "dtype": "float16"})
+            elif isinstance(a, list):
+                values.append({"type": "list", "items": a})
+            else:
+                values.append({"type": "scalar", "value": a})
+            args.append(len(values) - 1)
+        outs = []
+        for s in out_shapes:
+            values.append({"type": "tensor", "shape": list(s), "dtype": out_dtype})
+            outs.append(len(values) - 1)
+        if len(outs) > 1:
+            values.append({"type": "tensorlist", "items": outs})
+            args.append(len(values) - 1)
+        else:
+            args.append(outs[0])
+        prog = {"version": "1", "chain": [{"name": name, "args": args}], "values": values,
+                "inputIds": [i for i, a in enumerate(args_vals) if isinstance(a, np.ndarray)],
+                "outputIds": outs, "memoryPlan": {"pools": []}}
+        return program_eval.evaluate(prog, b"", [a for a in args_vals if isinstance(a, np.ndarray)])
+
+    tx = torch.from_numpy(x)
+    f16 = lambda t: t.to(torch.float16).to(torch.float64).numpy()
+    assert np.array_equal(run("aten.sigmoid.default", [x], [x.shape])[0], f16(torch.sigmoid(tx)))
+    up = run("aten.upsample_nearest2d.vec", [x, [2, 2]], [(1, 6, 18, 14)])[0]
+    assert np.array_equal(up, F.interpolate(tx, scale_factor=2, mode="nearest").numpy())
+    mp = run("aten.max_pool2d_with_indices.default", [x, [5, 5], [1, 1], [2, 2], [1, 1], False],
+             [x.shape, x.shape])[0]
+    assert np.array_equal(mp, F.max_pool2d(tx, 5, 1, 2).numpy())
+    mp2 = run("aten.max_pool2d_with_indices.default", [x, [3, 3], [2, 2], [1, 1], [1, 1], False],
+              [(1, 6, 5, 4), (1, 6, 5, 4)])[0]
+    assert np.array_equal(mp2, F.max_pool2d(tx, 3, 2, 1).numpy())
+    sp = run("aten.split_with_sizes_copy.default", [x, [2, 4], 1], [(1, 2, 9, 7), (1, 4, 9, 7)])
+    assert np.array_equal(sp[0], x[:, :2]) and np.array_equal(sp[1], x[:, 2:])
+
+
+# ------------------------------------------------------------ GPU runs
+def _gpu_vs_cpu(Y, tmp_path, img):
+    from oracle import program_eval
+
+    Y.write(str(tmp_path), img=img)
+    out = tmp_path / "out.bin"
+    print(f"[yolo program] img={img}: running on GPU 0 through Node", flush=True)
+    r = subprocess.run([NODE, RUNNER, str(tmp_path), "--device", "0", "--warmup", "1", "--reps", "3",
+                        "--out", str(out)], capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, r.stderr[-3000:]
+    gpu = np.fromfile(out, dtype=np.float16).astype(np.float64)
+    prog = json.load(open(tmp_path / "program.json"))
+    weights = open(tmp_path / "weights.bin", "rb").read()
+    x = np.fromfile(tmp_path / "input.bin", dtype=np.float16).astype(np.float64)
+    ref = program_eval.evaluate(prog, weights, [x])[0].ravel()
+    assert gpu.shape == ref.shape and np.all(np.isfinite(gpu))
+    d = np.abs(gpu - ref)
+    # One rounding per op on both sides; the difference is accumulation order
+    # (fp32 on the GPU, fp64 here) propagated through ~30 layers of fp16.
+    rel = np.linalg.norm(gpu - ref) / np.linalg.norm(ref)
+    frac = np.mean(d > 0.02 + 0.02 * np.abs(ref))
+    print(f"[yolo program] img={img}: normwise rel err {rel:.2e}, max abs {d.max():.3e}, "
+          f"fraction outside 0.02+0.02|ref|: {frac:.2e}", flush=True)
+    # measured: rel ~6e-4, max abs ~6e-4 on outputs of magnitude ~0.5
+    assert rel < 3e-3
+    assert frac == 0.0 and d.max() < 1e-2
+
+
+@needs_node
+@pytest.mark.gpu
+def test_yolo_program_gpu_matches_cpu_160(Y, orc, tmp_path):
+    _gpu_vs_cpu(Y, tmp_path, 160)
+
+
+@needs_node
+@pytest.mark.gpu
+def test_yolo_program_gpu_matches_cpu_640(Y, orc, tmp_path):
+    _gpu_vs_cpu(Y, tmp_path, 640)
