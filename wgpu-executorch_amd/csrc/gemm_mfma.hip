@@ -136,7 +136,7 @@ __device__ __forceinline__ void st_b16(uint32_t v, rsrc_t r, uint32_t off) {
 // writes before the coalesced 16-byte global stores.
 template <int BM, int BN, int WGM, int WGN, int BMODE, bool AVEC, bool BVEC, bool BF>
 __global__ __launch_bounds__(WGM * WGN * 64)
-__attribute__((amdgpu_waves_per_eu(2))) void k_gemm(KParams p) {
+__attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 2))) void k_gemm(KParams p) {
   extern __shared__ uint4 smem_u4[];
   uint16_t* smem = reinterpret_cast<uint16_t*>(smem_u4);
   constexpr int NT = WGM * WGN * 64;
@@ -383,22 +383,28 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(KParams p) {
   f32x16 acc[TM][TN];
   const int frow = lane & 31;
   const int fk = (lane >> 5) * 8;
+  // Fragments are software-pipelined: the LDS reads for k step kk+1 are
+  // issued before the MFMAs of step kk, so their latency hides behind them.
   auto compute_slice = [&](int stage) {
     const uint16_t* sa = smem + stage * STAGE;
     const uint16_t* sb = sa + BM * RS;
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      uint4 af[TM], bfr[TN];
+    uint4 af[2][TM], bfr[2][TN];
+    auto frags = [&](int kk, uint4* a, uint4* b) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const uint4*>(sa + (wm * WM + i * 32 + frow) * RS + kk * 16 + fk);
+        a[i] = *reinterpret_cast<const uint4*>(sa + (wm * WM + i * 32 + frow) * RS + kk * 16 + fk);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        bfr[j] = *reinterpret_cast<const uint4*>(sb + (wn * WN + j * 32 + frow) * RS + kk * 16 + fk);
+        b[j] = *reinterpret_cast<const uint4*>(sb + (wn * WN + j * 32 + frow) * RS + kk * 16 + fk);
+    };
+    frags(0, af[0], bfr[0]);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      if (kk + 1 < BK / 16) frags(kk + 1, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma<BF>(bfr[j], af[i], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma<BF>(bfr[kk & 1][j], af[kk & 1][i], acc[i][j]);
     }
   };
 
@@ -430,6 +436,18 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(KParams p) {
     store_slice((t + 1) & 1, Rn);
     load_slice(cur, (t + 3) * BK, Rn);
     compute_slice(t & 1);
+#ifdef WGX_INTERLEAVE
+    // Spread the slice's LDS writes and global loads between its MFMAs
+    // (they were issued first in program order) so the matrix pipe keeps
+    // being fed while they go out.
+#pragma unroll
+    for (int q = 0; q < TM * TN * (BK / 16); ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // one LDS write
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+    }
+#endif
     __syncthreads();
   };
 
@@ -529,6 +547,400 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(KParams p) {
   }
 }
 
+// ============================================================ pipelined kernel
+// The main kernel for 16-byte-aligned A.  A (and B in the B_NK form) stream
+// from global memory straight into LDS with buffer_load ... lds (LDS-DMA: no
+// registers in between), through three LDS stages: while slice t is
+// multiplied, slices t+1 and t+2 are in flight.  Each stage is its own
+// __shared__ array, so the compiler can tell that reading stage t does not
+// touch the stages being filled and inserts no wait for them; the kernel
+// waits explicitly (vmcnt) for exactly the slice it needs next.  B in the
+// B_KN / B_CONV forms (a transpose or a gather) goes through registers, one
+// slice ahead.  Tiles in LDS are [rows][64] 16-bit elements, 128-byte rows,
+// with the 16-byte chunk c of row r stored at chunk c ^ (r & 7): the eight
+// rows a fragment read touches per cycle then hit eight different bank
+// groups.  The epilogue writes C straight from the accumulators (each lane
+// owns 4 consecutive columns of a row per register group), so the next
+// tile's first slices can be in flight during it.
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One LDS-DMA load: 16 bytes per lane from buffer offset voff into LDS at
+// lds_wave_base + 16 * lane.  Written as inline asm so the compiler does not
+// track it: every wait for these loads is the explicit wait_vm<> below, and
+// the compiler does not add a conservative vmcnt(0) before each LDS read.
+// The "memory" clobber keeps LDS accesses from moving across it.  One wait
+// state separates the M0 write from the instruction that reads M0.
+__device__ __forceinline__ void dma16(rsrc_t r, const uint16_t* lds_wave_base, uint32_t voff) {
+  const uint32_t la = (uint32_t)(uintptr_t)lds_wave_base;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(la), "v"(voff), "s"(r) : "memory", "m0");
+}
+__device__ __forceinline__ void st_b64(uint2 v, rsrc_t r, uint32_t off) {
+  using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+  const u32x2 d = {v.x, v.y};
+  __builtin_amdgcn_raw_buffer_store_b64(d, r, (int)off, 0, 0);
+}
+// s_waitcnt vmcnt(n) with lgkmcnt / expcnt left unconstrained (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+
+template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, bool BF>
+__global__ __launch_bounds__(WGM * WGN * 64)
+__attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 2))) void k_gemm3(KParams p) {
+  constexpr int NT = WGM * WGN * 64, NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int BK = 64;
+  constexpr int BMAX = BM > BN ? BM : BN;
+  constexpr bool BDMA = BMODE == B_NK;
+  constexpr int CHA = BM * 8 / NT;             // A: DMA instructions per thread per slice
+  constexpr int CHB = BDMA ? BN * 8 / NT : 0;  // B (B_NK): same
+  constexpr int DMAS = CHA + CHB;              // DMA loads per thread per slice
+  constexpr bool KNV = BMODE == B_KN && BVEC;
+  constexpr int NKB = KNV ? (2 * BN + NT - 1) / NT : 1;
+  constexpr int KR = BK * BN / NT;             // column loaders (B_KN scalar / B_CONV)
+  constexpr int RBV = KNV ? 4 * NKB : 1;
+  constexpr int RBS = (BDMA || KNV) ? 1 : KR / 2;
+  static_assert(TM >= 1 && TN >= 1 && CHA >= 1 && (BM * 8) % NT == 0, "tile shape");
+  static_assert(!BDMA || (BN * 8) % NT == 0, "B tile shape");
+  static_assert(BDMA || KNV || (BN >= 64 && KR % 8 == 0), "column loader needs BN >= 64");
+  static_assert(DMAS < 64, "vmcnt");
+
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * BK], sA1[BM * BK], sA2[BM * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * BK], sB1[BN * BK], sB2[BN * BK];
+  __shared__ __attribute__((aligned(16))) float sbias[2][BMAX];
+  extern __shared__ uint32_t ktab_lds[];  // B_CONV: per-k (offset << 6) | tap
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int M = p.M, N = p.N, K = p.K;
+  const int KT = (K + BK - 1) / BK;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_mn = tiles_m * p.tiles_n;
+  const int ntiles = tiles_mn * p.batch;
+  const int G = gridDim.x;
+  const int rb = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+
+  if constexpr (BMODE == B_CONV) {
+    for (int i = tid; i < KT * BK; i += NT) ktab_lds[i] = p.ktab[i];
+    __syncthreads();
+  }
+
+  // DMA lane mapping: instruction i of wave w fills LDS chunks
+  // (i*NW + w)*64 + lane, i.e. row (i*NW + w)*8 + lane/8, stored chunk lane%8,
+  // which holds logical chunk (lane%8) ^ (row%8).
+  const int dchunk = (lane & 7) ^ ((lane >> 3) & 7);
+  auto stA = [&](auto s) -> uint16_t* {
+    if constexpr (decltype(s)::value == 0) return sA0;
+    else if constexpr (decltype(s)::value == 1) return sA1;
+    else return sA2;
+  };
+  auto stB = [&](auto s) -> uint16_t* {
+    if constexpr (decltype(s)::value == 0) return sB0;
+    else if constexpr (decltype(s)::value == 1) return sB1;
+    else return sB2;
+  };
+
+  struct TileState {
+    rsrc_t ra, rb;
+    int m0, n0, z, gn_col, colbase;
+    unsigned long long cmask;
+    uint32_t bias_h;
+  };
+  const int nl = tid % BN;
+  const int krun = tid / BN;
+  auto tile_state = [&](int tile) {
+    TileState s;
+    const int z = tile / tiles_mn, r = tile % tiles_mn;
+    const int gsz = p.gm * p.tiles_n;
+    const int grp = r / gsz, rr = r - grp * gsz;
+    const int gmh = min(p.gm, tiles_m - grp * p.gm);
+    s.m0 = (grp * p.gm + rr % gmh) * BM;
+    s.n0 = (rr / gmh) * BN;
+    s.z = z;
+    const int mrows = min(BM, M - s.m0);
+    s.ra = make_rsrc(p.A + (long long)z * p.sA + (long long)s.m0 * p.lda,
+                     (uint32_t)((mrows - 1) * p.lda + K) * 2u);
+    if constexpr (BMODE == B_NK) {
+      const int nrows = min(BN, N - s.n0);
+      s.rb = make_rsrc(p.B + (long long)z * p.sB + (long long)s.n0 * p.ldb,
+                       (uint32_t)((nrows - 1) * p.ldb + K) * 2u);
+    } else if constexpr (BMODE == B_CONV) {
+      s.rb = make_rsrc(p.B + (long long)z * p.sB, p.b_bytes);
+    } else {
+      s.rb = make_rsrc(p.B, 0u);
+    }
+    s.bias_h = 0u;
+    if (p.bias_mode != BIAS_NONE) {
+      const bool col = p.bias_mode == BIAS_COL;
+      const int lim = col ? N : M, b0 = col ? s.n0 : s.m0, cnt = col ? BN : BM;
+      const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)lim * 2u);
+      s.bias_h = ld_b16(rbias, (tid < cnt && b0 + tid < lim) ? (uint32_t)(b0 + tid) * 2u : OOB);
+    }
+    s.gn_col = s.n0 + nl;
+    s.colbase = 0;
+    s.cmask = 0ull;
+    if constexpr (BMODE == B_CONV) {
+      if (s.gn_col < N) {
+        const ConvGeom& g = p.g;
+        const int oh = s.gn_col / g.OW, ow = s.gn_col - oh * g.OW;
+        const int ih0 = oh * g.sH - g.pH, iw0 = ow * g.sW - g.pW;
+        s.colbase = ih0 * g.IW + iw0;
+        for (int kh = 0; kh < g.KH; ++kh) {
+          const int ih = ih0 + kh * g.dH;
+          if (ih < 0 || ih >= g.IH) continue;
+          for (int kw = 0; kw < g.KW; ++kw) {
+            const int iw = iw0 + kw * g.dW;
+            if (iw >= 0 && iw < g.IW) s.cmask |= 1ull << (kh * g.KW + kw);
+          }
+        }
+      }
+    }
+    return s;
+  };
+
+  // ---------------------------------------------------------- loads
+  // DMA of a k-contiguous operand slice into stage array dst: CH instructions
+  auto dma_rows = [&](rsrc_t rs, long long ld, int k0, uint16_t* dst, auto ch_tag) {
+    constexpr int CH = decltype(ch_tag)::value;
+    const bool kok = k0 + dchunk * 8 < K;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int row = (i * NW + wave) * 8 + (lane >> 3);
+      const uint32_t off = (uint32_t)(row * ld + k0 + dchunk * 8) * 2u;
+      dma16(rs, dst + (i * NW + wave) * 512, kok ? off : OOB);
+    }
+  };
+  struct BRegs {
+    uint4 bv[RBV];
+    uint32_t bs[RBS];
+  };
+  // register-staged B (B_KN / B_CONV): global -> registers
+  auto load_b = [&](const TileState& st, int k0, BRegs& R) {
+    if constexpr (BMODE == B_KN) {
+      const int krows = min(BK, K - k0);
+      const int kb0 = krows > 0 ? k0 : 0;
+      const rsrc_t rs = make_rsrc(p.B + (long long)st.z * p.sB + (long long)kb0 * p.ldb + st.n0,
+                                  krows > 0 ? (uint32_t)((krows - 1) * p.ldb + (N - st.n0)) * 2u : 0u);
+      if constexpr (KNV) {
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) {
+          const int c = tid + i * NT;
+          if (2 * BN % NT != 0 && c >= 2 * BN) break;  // wave-uniform
+          const int kg = c & 15, ng = c >> 4;
+          const bool nok = st.n0 + ng * 8 < N;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int kr = kg * 4 + j;
+            R.bv[4 * i + j] = ld_b128(rs, (nok && kr < krows) ? (uint32_t)(kr * p.ldb + ng * 8) * 2u : OOB);
+          }
+        }
+      } else {
+        const int kb = krun * KR;
+        const bool nok = st.gn_col < N;
+        uint32_t v[KR];
+#pragma unroll
+        for (int e = 0; e < KR; ++e)
+          v[e] = ld_b16(rs, (nok && kb + e < krows) ? (uint32_t)((kb + e) * p.ldb + nl) * 2u : OOB);
+#pragma unroll
+        for (int e = 0; e < KR; e += 2) R.bs[e / 2] = pack2(v[e], v[e + 1]);
+      }
+    } else if constexpr (BMODE == B_CONV) {
+      const bool live = k0 < K;
+      const unsigned long long lmask = live ? st.cmask : 0ull;
+      const uint32_t* tl = ktab_lds + (live ? k0 : 0) + krun * KR;
+      uint32_t ent[KR];
+#pragma unroll
+      for (int q = 0; q < KR; q += 4) {
+        const uint4 e4 = *reinterpret_cast<const uint4*>(tl + q);
+        ent[q] = e4.x;
+        ent[q + 1] = e4.y;
+        ent[q + 2] = e4.z;
+        ent[q + 3] = e4.w;
+      }
+      uint32_t v[KR];
+#pragma unroll
+      for (int e = 0; e < KR; ++e) {
+        const bool ok = (lmask >> (ent[e] & 63u)) & 1ull;
+        v[e] = ld_b16(st.rb, ok ? (uint32_t)(st.colbase + (int)(ent[e] >> 6)) * 2u : OOB);
+      }
+#pragma unroll
+      for (int e = 0; e < KR; e += 2) R.bs[e / 2] = pack2(v[e], v[e + 1]);
+    }
+  };
+  // registers -> LDS (swizzled [n][k] layout)
+  auto store_b = [&](uint16_t* sb, const BRegs& R) {
+    if constexpr (KNV) {
+#pragma unroll
+      for (int i = 0; i < NKB; ++i) {
+        const int c = tid + i * NT;
+        if (2 * BN % NT != 0 && c >= 2 * BN) break;  // wave-uniform
+        const int kg = c & 15, ng = c >> 4;
+        const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 0]);
+        const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 1]);
+        const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 2]);
+        const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 3]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = e >> 1;
+          uint2 col;
+          if (e & 1) {
+            col.x = (r0[d] >> 16) | (r1[d] & 0xffff0000u);
+            col.y = (r2[d] >> 16) | (r3[d] & 0xffff0000u);
+          } else {
+            col.x = (r0[d] & 0xffffu) | (r1[d] << 16);
+            col.y = (r2[d] & 0xffffu) | (r3[d] << 16);
+          }
+          const int n = ng * 8 + e;
+          // k = kg*4 .. kg*4+3: chunk kg/2, half (kg&1) of it
+          *reinterpret_cast<uint2*>(sb + swz(n, kg >> 1) + (kg & 1) * 4) = col;
+        }
+      }
+    } else if constexpr (!BDMA) {
+#pragma unroll
+      for (int q = 0; q < KR / 8; ++q)
+        *reinterpret_cast<uint4*>(sb + swz(nl, krun * (KR / 8) + q)) =
+            make_uint4(R.bs[4 * q], R.bs[4 * q + 1], R.bs[4 * q + 2], R.bs[4 * q + 3]);
+    }
+  };
+
+  // ---------------------------------------------------------- compute
+  f32x16 acc[TM][TN];
+  const int frow = lane & 31;
+  const int fc = lane >> 5;  // logical chunk within a 16-k step
+  auto compute = [&](const uint16_t* sa, const uint16_t* sb) {
+    uint4 af[2][TM], bfr[2][TN];
+    auto frags = [&](int kk, uint4* a, uint4* b) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        a[i] = *reinterpret_cast<const uint4*>(sa + swz(wm * WM + i * 32 + frow, kk * 2 + fc));
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        b[j] = *reinterpret_cast<const uint4*>(sb + swz(wn * WN + j * 32 + frow, kk * 2 + fc));
+    };
+    frags(0, af[0], bfr[0]);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      if (kk + 1 < BK / 16) frags(kk + 1, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma<BF>(bfr[kk & 1][j], af[kk & 1][i], acc[i][j]);
+    }
+  };
+
+  int tile = rb;
+  if (tile >= ntiles) return;
+  TileState cur = tile_state(tile);
+  BRegs RB;
+
+  // slices 0 and 1 of a tile: DMA into stages 0 and 1; register-staged B
+  // slice 0 goes to LDS at once, slice 1 stays in registers
+  auto prologue = [&](const TileState& st) {
+    if constexpr (!BDMA) load_b(st, 0, RB);
+    dma_rows(st.ra, p.lda, 0, stA(std::integral_constant<int, 0>{}), std::integral_constant<int, CHA>{});
+    if constexpr (BDMA)
+      dma_rows(st.rb, p.ldb, 0, stB(std::integral_constant<int, 0>{}), std::integral_constant<int, CHB>{});
+    dma_rows(st.ra, p.lda, BK, stA(std::integral_constant<int, 1>{}), std::integral_constant<int, CHA>{});
+    if constexpr (BDMA)
+      dma_rows(st.rb, p.ldb, BK, stB(std::integral_constant<int, 1>{}), std::integral_constant<int, CHB>{});
+  };
+
+  // Step t (stage s = t % 3): request slice t+2 into stage (t+2) % 3 (read
+  // last in step t-1, which ended with a barrier), multiply stage s, then
+  // wait until slice t+1 has landed and publish it with a barrier.
+  auto step = [&](int t, auto s_tag) {
+    constexpr int S = decltype(s_tag)::value;
+    constexpr int S1 = (S + 1) % 3, S2 = (S + 2) % 3;
+    using I1 = std::integral_constant<int, S1>;
+    using I2 = std::integral_constant<int, S2>;
+    if constexpr (!BDMA) load_b(cur, (t + 1) * BK, RB);
+    dma_rows(cur.ra, p.lda, (t + 2) * BK, stA(I2{}), std::integral_constant<int, CHA>{});
+    if constexpr (BDMA) dma_rows(cur.rb, p.ldb, (t + 2) * BK, stB(I2{}), std::integral_constant<int, CHB>{});
+    compute(stA(s_tag), stB(s_tag));
+    if constexpr (!BDMA) store_b(stB(I1{}), RB);
+    wait_vm<DMAS>();  // slice t+1's DMA is done, slice t+2's may still run
+    __syncthreads();
+  };
+
+  prologue(cur);
+  while (true) {
+    const int par = (tile / G) & 1;  // bias buffer of this tile
+    if constexpr (!BDMA) store_b(stB(std::integral_constant<int, 0>{}), RB);
+    if (p.bias_mode != BIAS_NONE && tid < BMAX) sbias[par][tid] = p.beta * ld_f32<BF>((uint16_t)cur.bias_h);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    wait_vm<DMAS>();  // slice 0 landed (slice 1 may still run)
+    __syncthreads();
+
+    for (int t = 0; t < KT; t += 3) {
+      step(t, std::integral_constant<int, 0>{});
+      if (t + 1 < KT) step(t + 1, std::integral_constant<int, 1>{});
+      if (t + 2 < KT) step(t + 2, std::integral_constant<int, 2>{});
+    }
+    // the DMAs of the two slices past K (zeros) land before stages 0 and 1
+    // are refilled for the next tile
+    wait_vm<0>();
+    __syncthreads();
+
+    const int m0 = cur.m0, n0 = cur.n0, z = cur.z;
+    const int next = tile + G;
+    if (next < ntiles) {  // the next tile's first slices run under this epilogue
+      cur = tile_state(next);
+      prologue(cur);
+    }
+
+    // ------------------------------------------------------ epilogue
+    // acc[i][j] holds C^T: lane owns row m = i*32 + lane%32 and, per register
+    // group g, the 4 columns n = j*32 + 8g + 4*(lane/32) + (0..3).
+    const int mrows = min(BM, M - m0);
+    const rsrc_t rc = make_rsrc(p.C + (long long)z * p.sC + (long long)m0 * p.ldc + n0,
+                                (uint32_t)((mrows - 1) * p.ldc + (N - n0)) * 2u);
+    const bool cvec = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 7) == 0) &&
+                      ((p.sC & 3) == 0) && ((N & 3) == 0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = wm * WM + i * 32 + frow;
+      const float rowb = p.bias_mode == BIAS_ROW ? sbias[par][row] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+          float4 bc = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (p.bias_mode == BIAS_COL) bc = *reinterpret_cast<const float4*>(&sbias[par][col]);
+          const float bb[4] = {bc.x, bc.y, bc.z, bc.w};
+          uint32_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
+            if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+            h[e] = st_bits<BF>(x);
+          }
+          const uint32_t off = (uint32_t)(row * p.ldc + col) * 2u;
+          if (cvec) {
+            st_b64(make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3])), rc, n0 + col < N ? off : OOB);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) st_b16(h[e], rc, n0 + col + e < N ? off + 2u * e : OOB);
+          }
+        }
+    }
+    if (next >= ntiles) break;
+    tile = next;
+  }
+}
+
 int device_cus() {
   static int cus = 0;
   if (!cus) {
@@ -577,16 +989,56 @@ hipError_t launch_one(const KParams& kp, int batch, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, bool BF>
+hipError_t launch_one3(const KParams& kp, int batch, hipStream_t s) {
+  auto fn = k_gemm3<BM, BN, WGM, WGN, BMODE, BVEC, BF>;
+  const size_t dyn = BMODE == B_CONV ? (size_t)conv_ktab_rows(kp.K) * sizeof(uint32_t) : 0;
+  constexpr size_t stat = (size_t)3 * (BM + BN) * 64 * 2 + 2 * (BM > BN ? BM : BN) * 4;
+  if (stat + dyn > 160 * 1024) return hipErrorInvalidValue;
+  static bool attr_set = false;
+  if (!attr_set && s != name_only()) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)(160 * 1024 - stat));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  if (is_dry(s)) return hipSuccess;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
+                                                   WGM * WGN * 64, dyn) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  const long long ntiles = (long long)((kp.M + BM - 1) / BM) * kp.tiles_n * batch;
+  long long grid = (long long)device_cus() * per_cu;
+  if (grid > ntiles) grid = ntiles;
+  KParams k2 = kp;
+  k2.batch = batch;
+  {
+    const int tiles_m = (kp.M + BM - 1) / BM;
+    const double per_xcd = (double)(grid < 8 ? 1 : grid / 8);
+    int gm = (int)lround(sqrt(per_xcd * BN / BM));
+    k2.gm = gm < 1 ? 1 : (gm > tiles_m ? tiles_m : gm);
+  }
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WGM * WGN * 64), dyn, s, k2);
+  return hipGetLastError();
+}
+
 struct Tile {
   int bm, bn, wgm, wgn;
+  bool autosel = true;  // considered by the automatic choice
 };
 
-constexpr Tile kTiles[] = {{256, 128, 4, 2}, {128, 256, 2, 4}, {128, 128, 2, 2}, {128, 64, 2, 2},
-                           {64, 64, 2, 2}};
+constexpr Tile kTiles[] = {{256, 128, 4, 2},        {128, 256, 2, 4},        {256, 256, 2, 2, false},
+                           {256, 128, 2, 2, false}, {128, 256, 2, 2, false}, {128, 128, 2, 2},
+                           {128, 64, 2, 2},         {64, 64, 2, 2}};
 
+bool use_v2();
+
+// LDS bytes of a block: three unpadded stages (pipelined kernel) or two padded
+// ones (register-staged kernel), the bias buffers and the im2col table.
 size_t tile_lds(const Tile& t, int bmode, int K) {
-  return (size_t)2 * (t.bm + t.bn) * RS * 2 + (size_t)(t.bm > t.bn ? t.bm : t.bn) * 4 +
-         (bmode == B_CONV ? (size_t)conv_ktab_rows(K) * 4 : 0);
+  const size_t stages = use_v2() ? (size_t)2 * (t.bm + t.bn) * RS * 2 : (size_t)3 * (t.bm + t.bn) * 64 * 2;
+  return stages + (size_t)(t.bm > t.bn ? t.bm : t.bn) * 8 + (bmode == B_CONV ? (size_t)conv_ktab_rows(K) * 4 : 0);
 }
 
 // Picks the block tile: fewest rounds over the 256 CUs (a block of 8 waves
@@ -595,18 +1047,18 @@ size_t tile_lds(const Tile& t, int bmode, int K) {
 Tile choose_tile(int M, int N, int K, int batch, bool avec, int bmode) {
   if (!avec) return {64, 64, 2, 2};
   const char* force = getenv("WGX_MFMA_TILE");
-  if (force) {
-    int bm = 0, bn = 0;
-    if (sscanf(force, "%dx%d", &bm, &bn) == 2)
+  if (force) {  // "BMxBNwW": block tile and wave count
+    int bm = 0, bn = 0, w = 0;
+    if (sscanf(force, "%dx%dw%d", &bm, &bn, &w) == 3)
       for (const Tile& t : kTiles)
-        if (t.bm == bm && t.bn == bn && tile_lds(t, bmode, K) <= 160 * 1024) return t;
+        if (t.bm == bm && t.bn == bn && t.wgm * t.wgn == w && tile_lds(t, bmode, K) <= 160 * 1024) return t;
   }
   double best = 1e300;
   Tile bt = {64, 64, 2, 2};
   for (const Tile& t : kTiles) {
-    if (tile_lds(t, bmode, K) > 160 * 1024) continue;
+    if (!t.autosel || tile_lds(t, bmode, K) > 160 * 1024) continue;
     const long long tiles = (long long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
-    const int per_cu = t.wgm * t.wgn == 8 ? 1 : 2;
+    const int per_cu = t.wgm * t.wgn == 8 || tile_lds(t, bmode, K) > 80 * 1024 ? 1 : 2;
     const double rounds = ceil((double)tiles / (256.0 * per_cu));
     const double eff = 1.0 + 64.0 / t.bm + 64.0 / t.bn;
     const double cost = rounds * t.bm * t.bn * per_cu * eff;
@@ -618,10 +1070,33 @@ Tile choose_tile(int M, int N, int K, int batch, bool avec, int bmode) {
   return bt;
 }
 
+bool use_v2() {
+  static int v = -1;
+  if (v < 0) v = getenv("WGX_GEMM_V2") ? 1 : 0;
+  return v == 1;
+}
+
 template <int BMODE, bool AVEC, bool BVEC, bool BF>
 hipError_t dispatch_tile(const Tile& t, const KParams& kp, int batch, hipStream_t s) {
-  if (t.bm == 256 && t.bn == 128) return launch_one<256, 128, 4, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
-  if (t.bm == 128 && t.bn == 256) return launch_one<128, 256, 2, 4, BMODE, AVEC, BVEC, BF>(kp, batch, s);
+  const int w = t.wgm * t.wgn;
+  if constexpr (AVEC) {
+    if (!use_v2()) {
+      if (t.bm == 256 && t.bn == 128 && w == 8) return launch_one3<256, 128, 4, 2, BMODE, BVEC, BF>(kp, batch, s);
+      if (t.bm == 128 && t.bn == 256 && w == 8) return launch_one3<128, 256, 2, 4, BMODE, BVEC, BF>(kp, batch, s);
+      if (t.bm == 256 && t.bn == 128) return launch_one3<256, 128, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
+      if (t.bm == 128 && t.bn == 256) return launch_one3<128, 256, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
+      if (t.bm == 128 && t.bn == 128) return launch_one3<128, 128, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
+      if (t.bm == 128 && t.bn == 64) return launch_one3<128, 64, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
+      if (t.bm == 64 && t.bn == 64) return launch_one3<64, 64, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
+    }
+  }
+  if (t.bm == 256 && t.bn == 128 && w == 8) return launch_one<256, 128, 4, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
+  if (t.bm == 128 && t.bn == 256 && w == 8) return launch_one<128, 256, 2, 4, BMODE, AVEC, BVEC, BF>(kp, batch, s);
+  if constexpr (BMODE != B_CONV) {
+    if (t.bm == 256 && t.bn == 256) return launch_one<256, 256, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
+  }
+  if (t.bm == 256 && t.bn == 128) return launch_one<256, 128, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
+  if (t.bm == 128 && t.bn == 256) return launch_one<128, 256, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
   if (t.bm == 128 && t.bn == 128) return launch_one<128, 128, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
   if (t.bm == 128 && t.bn == 64) return launch_one<128, 64, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
   return launch_one<64, 64, 2, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
@@ -680,8 +1155,9 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
   if (name) {
     char buf[96];
     static const char* modes[] = {"nk", "kn", "conv"};
-    snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%d_%s%s%s", bf ? "bf16" : "f16", t.bm, t.bn,
-             modes[d.bmode], d.bmode == B_KN ? (knv ? "4x8" : "col") : "", avec ? "" : "_scalarA");
+    snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw%d_%s%s%s", bf ? "bf16" : "f16", t.bm, t.bn,
+             t.wgm * t.wgn, modes[d.bmode], d.bmode == B_KN ? (knv ? "4x8" : "col") : "",
+             avec ? "" : "_scalarA");
     *name = buf;
   }
   if (bf && d.bmode == B_CONV) return hipErrorInvalidValue;  // bf16 convolution is not offered
