@@ -586,9 +586,12 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
-__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+// gfx950 LDS serves a 128-bit read 16 lanes (256 bytes, 64 banks) at a time;
+// 16 consecutive rows are 8 row pairs sharing a 256-byte bank period, so the
+// swizzle keys on the pair index: chunk c of row r is stored at c ^ ((r/2) % 8).
+__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 7)) << 3); }
 
-template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, bool BF>
+template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, bool BF, int NS>
 __global__ __launch_bounds__(WGM * WGN * 64)
 __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 2))) void k_gemm3(KParams p) {
   constexpr int NT = WGM * WGN * 64, NW = WGM * WGN;
@@ -608,10 +611,12 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
   static_assert(TM >= 1 && TN >= 1 && CHA >= 1 && (BM * 8) % NT == 0, "tile shape");
   static_assert(!BDMA || (BN * 8) % NT == 0, "B tile shape");
   static_assert(BDMA || KNV || (BN >= 64 && KR % 8 == 0), "column loader needs BN >= 64");
-  static_assert(DMAS < 64, "vmcnt");
+  static_assert((NS - 2) * DMAS < 64, "vmcnt");
 
+  static_assert(NS == 3 || NS == 4, "stages");
   __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * BK], sA1[BM * BK], sA2[BM * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * BK], sB1[BN * BK], sB2[BN * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA3[NS > 3 ? BM * BK : 8], sB3[NS > 3 ? BN * BK : 8];
   __shared__ __attribute__((aligned(16))) float sbias[2][BMAX];
   extern __shared__ uint32_t ktab_lds[];  // B_CONV: per-k (offset << 6) | tap
 
@@ -634,17 +639,18 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
 
   // DMA lane mapping: instruction i of wave w fills LDS chunks
   // (i*NW + w)*64 + lane, i.e. row (i*NW + w)*8 + lane/8, stored chunk lane%8,
-  // which holds logical chunk (lane%8) ^ (row%8).
-  const int dchunk = (lane & 7) ^ ((lane >> 3) & 7);
+  // which holds logical chunk (lane%8) ^ ((row/2)%8) (see swz).
   auto stA = [&](auto s) -> uint16_t* {
     if constexpr (decltype(s)::value == 0) return sA0;
     else if constexpr (decltype(s)::value == 1) return sA1;
-    else return sA2;
+    else if constexpr (decltype(s)::value == 2) return sA2;
+    else return sA3;
   };
   auto stB = [&](auto s) -> uint16_t* {
     if constexpr (decltype(s)::value == 0) return sB0;
     else if constexpr (decltype(s)::value == 1) return sB1;
-    else return sB2;
+    else if constexpr (decltype(s)::value == 2) return sB2;
+    else return sB3;
   };
 
   struct TileState {
@@ -709,12 +715,12 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
   // DMA of a k-contiguous operand slice into stage array dst: CH instructions
   auto dma_rows = [&](rsrc_t rs, long long ld, int k0, uint16_t* dst, auto ch_tag) {
     constexpr int CH = decltype(ch_tag)::value;
-    const bool kok = k0 + dchunk * 8 < K;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int row = (i * NW + wave) * 8 + (lane >> 3);
-      const uint32_t off = (uint32_t)(row * ld + k0 + dchunk * 8) * 2u;
-      dma16(rs, dst + (i * NW + wave) * 512, kok ? off : OOB);
+      const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+      const uint32_t off = (uint32_t)(row * ld + k0 + chunk * 8) * 2u;
+      dma16(rs, dst + (i * NW + wave) * 512, k0 + chunk * 8 < K ? off : OOB);
     }
   };
   struct BRegs {
@@ -850,22 +856,27 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     dma_rows(st.ra, p.lda, BK, stA(std::integral_constant<int, 1>{}), std::integral_constant<int, CHA>{});
     if constexpr (BDMA)
       dma_rows(st.rb, p.ldb, BK, stB(std::integral_constant<int, 1>{}), std::integral_constant<int, CHB>{});
+    if constexpr (NS > 3) {
+      dma_rows(st.ra, p.lda, 2 * BK, stA(std::integral_constant<int, 2>{}), std::integral_constant<int, CHA>{});
+      if constexpr (BDMA)
+        dma_rows(st.rb, p.ldb, 2 * BK, stB(std::integral_constant<int, 2>{}), std::integral_constant<int, CHB>{});
+    }
   };
 
-  // Step t (stage s = t % 3): request slice t+2 into stage (t+2) % 3 (read
-  // last in step t-1, which ended with a barrier), multiply stage s, then
-  // wait until slice t+1 has landed and publish it with a barrier.
+  // Step t (stage s = t % NS): request slice t+NS-1 into the stage read last
+  // in step t-1 (which ended with a barrier), multiply stage s, then wait
+  // until slice t+1 has landed and publish it with a barrier.
   auto step = [&](int t, auto s_tag) {
     constexpr int S = decltype(s_tag)::value;
-    constexpr int S1 = (S + 1) % 3, S2 = (S + 2) % 3;
+    constexpr int S1 = (S + 1) % NS, SL = (S + NS - 1) % NS;
     using I1 = std::integral_constant<int, S1>;
-    using I2 = std::integral_constant<int, S2>;
+    using IL = std::integral_constant<int, SL>;
     if constexpr (!BDMA) load_b(cur, (t + 1) * BK, RB);
-    dma_rows(cur.ra, p.lda, (t + 2) * BK, stA(I2{}), std::integral_constant<int, CHA>{});
-    if constexpr (BDMA) dma_rows(cur.rb, p.ldb, (t + 2) * BK, stB(I2{}), std::integral_constant<int, CHB>{});
+    dma_rows(cur.ra, p.lda, (t + NS - 1) * BK, stA(IL{}), std::integral_constant<int, CHA>{});
+    if constexpr (BDMA) dma_rows(cur.rb, p.ldb, (t + NS - 1) * BK, stB(IL{}), std::integral_constant<int, CHB>{});
     compute(stA(s_tag), stB(s_tag));
     if constexpr (!BDMA) store_b(stB(I1{}), RB);
-    wait_vm<DMAS>();  // slice t+1's DMA is done, slice t+2's may still run
+    wait_vm<(NS - 2) * DMAS>();  // slice t+1 landed, the later ones may still run
     __syncthreads();
   };
 
@@ -880,16 +891,18 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    wait_vm<DMAS>();  // slice 0 landed (slice 1 may still run)
+    wait_vm<(NS - 2) * DMAS>();  // slice 0 landed (slices 1.. may still run)
     __syncthreads();
 
-    for (int t = 0; t < KT; t += 3) {
+    for (int t = 0; t < KT; t += NS) {
       step(t, std::integral_constant<int, 0>{});
       if (t + 1 < KT) step(t + 1, std::integral_constant<int, 1>{});
       if (t + 2 < KT) step(t + 2, std::integral_constant<int, 2>{});
+      if constexpr (NS > 3)
+        if (t + 3 < KT) step(t + 3, std::integral_constant<int, 3 % NS>{});
     }
-    // the DMAs of the two slices past K (zeros) land before stages 0 and 1
-    // are refilled for the next tile
+    // the DMAs of the slices past K (zeros) land before the stages are
+    // refilled for the next tile
     wait_vm<0>();
     __syncthreads();
 
@@ -989,19 +1002,19 @@ hipError_t launch_one(const KParams& kp, int batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, bool BF>
+template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, bool BF, int NS = 3>
 hipError_t launch_one3(const KParams& kp, int batch, hipStream_t s) {
-  auto fn = k_gemm3<BM, BN, WGM, WGN, BMODE, BVEC, BF>;
+  auto fn = k_gemm3<BM, BN, WGM, WGN, BMODE, BVEC, BF, NS>;
   const size_t dyn = BMODE == B_CONV ? (size_t)conv_ktab_rows(kp.K) * sizeof(uint32_t) : 0;
-  constexpr size_t stat = (size_t)3 * (BM + BN) * 64 * 2 + 2 * (BM > BN ? BM : BN) * 4;
+  // static LDS: the stages and two bias buffers
+  constexpr size_t stat = (size_t)NS * (BM + BN) * 64 * 2 + 2 * (BM > BN ? BM : BN) * 4;
   if (stat + dyn > 160 * 1024) return hipErrorInvalidValue;
-  static bool attr_set = false;
-  if (!attr_set && s != name_only()) {
+  static size_t attr_dyn = 0;  // largest dynamic size allowed so far
+  if (dyn > attr_dyn && s != name_only()) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)(160 * 1024 - stat));
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_dyn = dyn;
   }
   if (is_dry(s)) return hipSuccess;
   int per_cu = 0;
