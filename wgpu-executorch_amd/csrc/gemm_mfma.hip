@@ -589,34 +589,72 @@ __device__ __forceinline__ void wait_vm() {
 // gfx950 LDS serves a 128-bit read 16 lanes (256 bytes, 64 banks) at a time;
 // 16 consecutive rows are 8 row pairs sharing a 256-byte bank period, so the
 // swizzle keys on the pair index: chunk c of row r is stored at c ^ ((r/2) % 8).
-__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 7)) << 3); }
+// Returns a byte offset into a [rows][128 B] tile.
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
-template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, bool BF, int NS>
+// Element types of the pipelined kernel.
+enum { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+
+__device__ __forceinline__ uint32_t ld_b32(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void st_b32(uint32_t v, rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ float to_f32(uint32_t bits) {
+  if constexpr (DT == DT_F32) return __uint_as_float(bits);
+  else if constexpr (DT == DT_BF16) return __uint_as_float(bits << 16);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+// One 16-byte fragment pair's worth of MFMAs: for 16-bit types one
+// v_mfma_f32_32x32x16 (8 k per lane); for fp32 four v_mfma_f32_32x32x2_f32,
+// component e of each lane's 4 consecutive k.  A and B fragments use the same
+// lane->k mapping, so any pairing of k across the four is a valid sum.
+template <int DT>
+__device__ __forceinline__ f32x16 mfma_frag(uint4 b, uint4 a, f32x16 c) {
+  if constexpr (DT == DT_F32) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(b.x), __uint_as_float(a.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(b.y), __uint_as_float(a.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(b.z), __uint_as_float(a.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(b.w), __uint_as_float(a.w), c, 0, 0, 0);
+    return c;
+  } else {
+    return mfma<DT == DT_BF16>(b, a, c);
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, int DT, int NS>
 __global__ __launch_bounds__(WGM * WGN * 64)
 __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 2))) void k_gemm3(KParams p) {
   constexpr int NT = WGM * WGN * 64, NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int BK = 64;
+  constexpr int ES = DT == DT_F32 ? 4 : 2;  // element bytes
+  constexpr int EPC = 16 / ES;              // elements per 16-byte chunk
+  constexpr int BK = 128 / ES;              // k per slice: one 128-byte row
   constexpr int BMAX = BM > BN ? BM : BN;
   constexpr bool BDMA = BMODE == B_NK;
   constexpr int CHA = BM * 8 / NT;             // A: DMA instructions per thread per slice
   constexpr int CHB = BDMA ? BN * 8 / NT : 0;  // B (B_NK): same
   constexpr int DMAS = CHA + CHB;              // DMA loads per thread per slice
   constexpr bool KNV = BMODE == B_KN && BVEC;
-  constexpr int NKB = KNV ? (2 * BN + NT - 1) / NT : 1;
+  constexpr int KGS = BK / 4;                  // 4-k groups per slice (transpose loader)
+  constexpr int NKB = KNV ? (2 * BN + NT - 1) / NT : 1;  // 4 k x EPC n blocks per thread
   constexpr int KR = BK * BN / NT;             // column loaders (B_KN scalar / B_CONV)
   constexpr int RBV = KNV ? 4 * NKB : 1;
-  constexpr int RBS = (BDMA || KNV) ? 1 : KR / 2;
+  constexpr int RBS = (BDMA || KNV) ? 1 : KR;
   static_assert(TM >= 1 && TN >= 1 && CHA >= 1 && (BM * 8) % NT == 0, "tile shape");
   static_assert(!BDMA || (BN * 8) % NT == 0, "B tile shape");
-  static_assert(BDMA || KNV || (BN >= 64 && KR % 8 == 0), "column loader needs BN >= 64");
+  static_assert(BDMA || KNV || (BN >= 64 && KR % EPC == 0), "column loader needs BN >= 64");
+  static_assert(NS == 3 || NS == 4, "stages");
   static_assert((NS - 2) * DMAS < 64, "vmcnt");
 
-  static_assert(NS == 3 || NS == 4, "stages");
-  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * BK], sA1[BM * BK], sA2[BM * BK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * BK], sB1[BN * BK], sB2[BN * BK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sA3[NS > 3 ? BM * BK : 8], sB3[NS > 3 ? BN * BK : 8];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * 64], sA1[BM * 64], sA2[BM * 64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * 64], sB1[BN * 64], sB2[BN * 64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA3[NS > 3 ? BM * 64 : 8], sB3[NS > 3 ? BN * 64 : 8];
   __shared__ __attribute__((aligned(16))) float sbias[2][BMAX];
   extern __shared__ uint32_t ktab_lds[];  // B_CONV: per-k (offset << 6) | tap
 
@@ -631,26 +669,26 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
   const int ntiles = tiles_mn * p.batch;
   const int G = gridDim.x;
   const int rb = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const char* Ab = reinterpret_cast<const char*>(p.A);
+  const char* Bb = reinterpret_cast<const char*>(p.B);
+  char* Cb = reinterpret_cast<char*>(p.C);
 
   if constexpr (BMODE == B_CONV) {
     for (int i = tid; i < KT * BK; i += NT) ktab_lds[i] = p.ktab[i];
     __syncthreads();
   }
 
-  // DMA lane mapping: instruction i of wave w fills LDS chunks
-  // (i*NW + w)*64 + lane, i.e. row (i*NW + w)*8 + lane/8, stored chunk lane%8,
-  // which holds logical chunk (lane%8) ^ ((row/2)%8) (see swz).
-  auto stA = [&](auto s) -> uint16_t* {
-    if constexpr (decltype(s)::value == 0) return sA0;
-    else if constexpr (decltype(s)::value == 1) return sA1;
-    else if constexpr (decltype(s)::value == 2) return sA2;
-    else return sA3;
+  auto stA = [&](auto s) -> char* {
+    if constexpr (decltype(s)::value == 0) return reinterpret_cast<char*>(sA0);
+    else if constexpr (decltype(s)::value == 1) return reinterpret_cast<char*>(sA1);
+    else if constexpr (decltype(s)::value == 2) return reinterpret_cast<char*>(sA2);
+    else return reinterpret_cast<char*>(sA3);
   };
-  auto stB = [&](auto s) -> uint16_t* {
-    if constexpr (decltype(s)::value == 0) return sB0;
-    else if constexpr (decltype(s)::value == 1) return sB1;
-    else if constexpr (decltype(s)::value == 2) return sB2;
-    else return sB3;
+  auto stB = [&](auto s) -> char* {
+    if constexpr (decltype(s)::value == 0) return reinterpret_cast<char*>(sB0);
+    else if constexpr (decltype(s)::value == 1) return reinterpret_cast<char*>(sB1);
+    else if constexpr (decltype(s)::value == 2) return reinterpret_cast<char*>(sB2);
+    else return reinterpret_cast<char*>(sB3);
   };
 
   struct TileState {
@@ -671,14 +709,14 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     s.n0 = (rr / gmh) * BN;
     s.z = z;
     const int mrows = min(BM, M - s.m0);
-    s.ra = make_rsrc(p.A + (long long)z * p.sA + (long long)s.m0 * p.lda,
-                     (uint32_t)((mrows - 1) * p.lda + K) * 2u);
+    s.ra = make_rsrc(Ab + ((long long)z * p.sA + (long long)s.m0 * p.lda) * ES,
+                     (uint32_t)((mrows - 1) * p.lda + K) * ES);
     if constexpr (BMODE == B_NK) {
       const int nrows = min(BN, N - s.n0);
-      s.rb = make_rsrc(p.B + (long long)z * p.sB + (long long)s.n0 * p.ldb,
-                       (uint32_t)((nrows - 1) * p.ldb + K) * 2u);
+      s.rb = make_rsrc(Bb + ((long long)z * p.sB + (long long)s.n0 * p.ldb) * ES,
+                       (uint32_t)((nrows - 1) * p.ldb + K) * ES);
     } else if constexpr (BMODE == B_CONV) {
-      s.rb = make_rsrc(p.B + (long long)z * p.sB, p.b_bytes);
+      s.rb = make_rsrc(Bb + (long long)z * p.sB * ES, p.b_bytes);
     } else {
       s.rb = make_rsrc(p.B, 0u);
     }
@@ -686,8 +724,9 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     if (p.bias_mode != BIAS_NONE) {
       const bool col = p.bias_mode == BIAS_COL;
       const int lim = col ? N : M, b0 = col ? s.n0 : s.m0, cnt = col ? BN : BM;
-      const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)lim * 2u);
-      s.bias_h = ld_b16(rbias, (tid < cnt && b0 + tid < lim) ? (uint32_t)(b0 + tid) * 2u : OOB);
+      const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)lim * ES);
+      const uint32_t off = (tid < cnt && b0 + tid < lim) ? (uint32_t)(b0 + tid) * ES : OOB;
+      s.bias_h = ES == 4 ? ld_b32(rbias, off) : ld_b16(rbias, off);
     }
     s.gn_col = s.n0 + nl;
     s.colbase = 0;
@@ -712,50 +751,53 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
   };
 
   // ---------------------------------------------------------- loads
-  // DMA of a k-contiguous operand slice into stage array dst: CH instructions
-  auto dma_rows = [&](rsrc_t rs, long long ld, int k0, uint16_t* dst, auto ch_tag) {
+  // DMA lane mapping: instruction i of wave w fills LDS chunks
+  // (i*NW + w)*64 + lane, i.e. row (i*NW + w)*8 + lane/8, stored chunk lane%8,
+  // which holds logical chunk (lane%8) ^ ((row/2)%8) (see swz).
+  auto dma_rows = [&](rsrc_t rs, long long ld, int k0, char* dst, auto ch_tag) {
     constexpr int CH = decltype(ch_tag)::value;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int row = (i * NW + wave) * 8 + (lane >> 3);
       const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-      const uint32_t off = (uint32_t)(row * ld + k0 + chunk * 8) * 2u;
-      dma16(rs, dst + (i * NW + wave) * 512, k0 + chunk * 8 < K ? off : OOB);
+      const uint32_t off = (uint32_t)(row * ld + k0 + chunk * EPC) * ES;
+      dma16(rs, reinterpret_cast<const uint16_t*>(dst + (i * NW + wave) * 1024),
+            k0 + chunk * EPC < K ? off : OOB);
     }
   };
   struct BRegs {
     uint4 bv[RBV];
     uint32_t bs[RBS];
   };
-  // register-staged B (B_KN / B_CONV): global -> registers
+  // register-staged B (B_KN / B_CONV): global -> registers, one element per
+  // bs[] entry (16-bit values zero-extended)
   auto load_b = [&](const TileState& st, int k0, BRegs& R) {
     if constexpr (BMODE == B_KN) {
-      const int krows = min(BK, K - k0);
+      const int krows = min(BK, K - k0);  // <= 0 past K: every load reads zero
       const int kb0 = krows > 0 ? k0 : 0;
-      const rsrc_t rs = make_rsrc(p.B + (long long)st.z * p.sB + (long long)kb0 * p.ldb + st.n0,
-                                  krows > 0 ? (uint32_t)((krows - 1) * p.ldb + (N - st.n0)) * 2u : 0u);
+      const rsrc_t rs = make_rsrc(Bb + ((long long)st.z * p.sB + (long long)kb0 * p.ldb + st.n0) * ES,
+                                  krows > 0 ? (uint32_t)((krows - 1) * p.ldb + (N - st.n0)) * ES : 0u);
       if constexpr (KNV) {
 #pragma unroll
         for (int i = 0; i < NKB; ++i) {
           const int c = tid + i * NT;
           if (2 * BN % NT != 0 && c >= 2 * BN) break;  // wave-uniform
-          const int kg = c & 15, ng = c >> 4;
-          const bool nok = st.n0 + ng * 8 < N;
+          const int kg = c % KGS, ng = c / KGS;
+          const bool nok = st.n0 + ng * EPC < N;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int kr = kg * 4 + j;
-            R.bv[4 * i + j] = ld_b128(rs, (nok && kr < krows) ? (uint32_t)(kr * p.ldb + ng * 8) * 2u : OOB);
+            R.bv[4 * i + j] = ld_b128(rs, (nok && kr < krows) ? (uint32_t)(kr * p.ldb + ng * EPC) * ES : OOB);
           }
         }
       } else {
         const int kb = krun * KR;
         const bool nok = st.gn_col < N;
-        uint32_t v[KR];
 #pragma unroll
-        for (int e = 0; e < KR; ++e)
-          v[e] = ld_b16(rs, (nok && kb + e < krows) ? (uint32_t)((kb + e) * p.ldb + nl) * 2u : OOB);
-#pragma unroll
-        for (int e = 0; e < KR; e += 2) R.bs[e / 2] = pack2(v[e], v[e + 1]);
+        for (int e = 0; e < KR; ++e) {
+          const uint32_t off = (nok && kb + e < krows) ? (uint32_t)((kb + e) * p.ldb + nl) * ES : OOB;
+          R.bs[e] = ES == 4 ? ld_b32(rs, off) : ld_b16(rs, off);
+        }
       }
     } else if constexpr (BMODE == B_CONV) {
       const bool live = k0 < K;
@@ -770,57 +812,67 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
         ent[q + 2] = e4.z;
         ent[q + 3] = e4.w;
       }
-      uint32_t v[KR];
 #pragma unroll
       for (int e = 0; e < KR; ++e) {
         const bool ok = (lmask >> (ent[e] & 63u)) & 1ull;
-        v[e] = ld_b16(st.rb, ok ? (uint32_t)(st.colbase + (int)(ent[e] >> 6)) * 2u : OOB);
+        const uint32_t off = ok ? (uint32_t)(st.colbase + (int)(ent[e] >> 6)) * ES : OOB;
+        R.bs[e] = ES == 4 ? ld_b32(st.rb, off) : ld_b16(st.rb, off);
       }
-#pragma unroll
-      for (int e = 0; e < KR; e += 2) R.bs[e / 2] = pack2(v[e], v[e + 1]);
     }
   };
   // registers -> LDS (swizzled [n][k] layout)
-  auto store_b = [&](uint16_t* sb, const BRegs& R) {
+  auto store_b = [&](char* sb, const BRegs& R) {
     if constexpr (KNV) {
 #pragma unroll
       for (int i = 0; i < NKB; ++i) {
         const int c = tid + i * NT;
         if (2 * BN % NT != 0 && c >= 2 * BN) break;  // wave-uniform
-        const int kg = c & 15, ng = c >> 4;
+        const int kg = c % KGS, ng = c / KGS;
         const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 0]);
         const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 1]);
         const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 2]);
         const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&R.bv[4 * i + 3]);
+        if constexpr (ES == 4) {
+          // 4 k-rows x 4 columns: column e is one whole chunk (k = kg*4 .. +3)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int d = e >> 1;
-          uint2 col;
-          if (e & 1) {
-            col.x = (r0[d] >> 16) | (r1[d] & 0xffff0000u);
-            col.y = (r2[d] >> 16) | (r3[d] & 0xffff0000u);
-          } else {
-            col.x = (r0[d] & 0xffffu) | (r1[d] << 16);
-            col.y = (r2[d] & 0xffffu) | (r3[d] << 16);
+          for (int e = 0; e < 4; ++e)
+            *reinterpret_cast<uint4*>(sb + swz(ng * 4 + e, kg)) = make_uint4(r0[e], r1[e], r2[e], r3[e]);
+        } else {
+          // 4 k-rows x 8 columns: column e gets 4 k = half of chunk kg/2
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int d = e >> 1;
+            uint2 col;
+            if (e & 1) {
+              col.x = (r0[d] >> 16) | (r1[d] & 0xffff0000u);
+              col.y = (r2[d] >> 16) | (r3[d] & 0xffff0000u);
+            } else {
+              col.x = (r0[d] & 0xffffu) | (r1[d] << 16);
+              col.y = (r2[d] & 0xffffu) | (r3[d] << 16);
+            }
+            *reinterpret_cast<uint2*>(sb + swz(ng * 8 + e, kg >> 1) + (kg & 1) * 8) = col;
           }
-          const int n = ng * 8 + e;
-          // k = kg*4 .. kg*4+3: chunk kg/2, half (kg&1) of it
-          *reinterpret_cast<uint2*>(sb + swz(n, kg >> 1) + (kg & 1) * 4) = col;
         }
       }
     } else if constexpr (!BDMA) {
 #pragma unroll
-      for (int q = 0; q < KR / 8; ++q)
-        *reinterpret_cast<uint4*>(sb + swz(nl, krun * (KR / 8) + q)) =
-            make_uint4(R.bs[4 * q], R.bs[4 * q + 1], R.bs[4 * q + 2], R.bs[4 * q + 3]);
+      for (int q = 0; q < KR / EPC; ++q) {
+        uint4 v;
+        if constexpr (ES == 4)
+          v = make_uint4(R.bs[4 * q], R.bs[4 * q + 1], R.bs[4 * q + 2], R.bs[4 * q + 3]);
+        else
+          v = make_uint4(pack2(R.bs[8 * q], R.bs[8 * q + 1]), pack2(R.bs[8 * q + 2], R.bs[8 * q + 3]),
+                         pack2(R.bs[8 * q + 4], R.bs[8 * q + 5]), pack2(R.bs[8 * q + 6], R.bs[8 * q + 7]));
+        *reinterpret_cast<uint4*>(sb + swz(nl, krun * (KR / EPC) + q)) = v;
+      }
     }
   };
 
   // ---------------------------------------------------------- compute
   f32x16 acc[TM][TN];
   const int frow = lane & 31;
-  const int fc = lane >> 5;  // logical chunk within a 16-k step
-  auto compute = [&](const uint16_t* sa, const uint16_t* sb) {
+  const int fc = lane >> 5;  // logical chunk within a k step
+  auto compute = [&](const char* sa, const char* sb) {
     uint4 af[2][TM], bfr[2][TN];
     auto frags = [&](int kk, uint4* a, uint4* b) {
 #pragma unroll
@@ -832,12 +884,12 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     };
     frags(0, af[0], bfr[0]);
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      if (kk + 1 < BK / 16) frags(kk + 1, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
+    for (int kk = 0; kk < 4; ++kk) {  // 4 steps of 2 chunks = one 128-byte row
+      if (kk + 1 < 4) frags(kk + 1, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma<BF>(bfr[kk & 1][j], af[kk & 1][i], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_frag<DT>(bfr[kk & 1][j], af[kk & 1][i], acc[i][j]);
     }
   };
 
@@ -846,8 +898,8 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
   TileState cur = tile_state(tile);
   BRegs RB;
 
-  // slices 0 and 1 of a tile: DMA into stages 0 and 1; register-staged B
-  // slice 0 goes to LDS at once, slice 1 stays in registers
+  // the first NS-1 slices of a tile: DMA into stages 0..NS-2; register-staged
+  // B slice 0 goes to LDS at the top of the tile loop, slice 1 in step 0
   auto prologue = [&](const TileState& st) {
     if constexpr (!BDMA) load_b(st, 0, RB);
     dma_rows(st.ra, p.lda, 0, stA(std::integral_constant<int, 0>{}), std::integral_constant<int, CHA>{});
@@ -884,7 +936,7 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
   while (true) {
     const int par = (tile / G) & 1;  // bias buffer of this tile
     if constexpr (!BDMA) store_b(stB(std::integral_constant<int, 0>{}), RB);
-    if (p.bias_mode != BIAS_NONE && tid < BMAX) sbias[par][tid] = p.beta * ld_f32<BF>((uint16_t)cur.bias_h);
+    if (p.bias_mode != BIAS_NONE && tid < BMAX) sbias[par][tid] = p.beta * to_f32<DT>(cur.bias_h);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -917,9 +969,9 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     // acc[i][j] holds C^T: lane owns row m = i*32 + lane%32 and, per register
     // group g, the 4 columns n = j*32 + 8g + 4*(lane/32) + (0..3).
     const int mrows = min(BM, M - m0);
-    const rsrc_t rc = make_rsrc(p.C + (long long)z * p.sC + (long long)m0 * p.ldc + n0,
-                                (uint32_t)((mrows - 1) * p.ldc + (N - n0)) * 2u);
-    const bool cvec = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 7) == 0) &&
+    const rsrc_t rc = make_rsrc(Cb + ((long long)z * p.sC + (long long)m0 * p.ldc + n0) * ES,
+                                (uint32_t)((mrows - 1) * p.ldc + (N - n0)) * ES);
+    const bool cvec = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & (4 * ES - 1)) == 0) &&
                       ((p.sC & 3) == 0) && ((N & 3) == 0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -938,14 +990,22 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
           for (int e = 0; e < 4; ++e) {
             float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
             if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
-            h[e] = st_bits<BF>(x);
+            if constexpr (DT == DT_F32) h[e] = __float_as_uint(x);
+            else h[e] = st_bits<DT == DT_BF16>(x);
           }
-          const uint32_t off = (uint32_t)(row * p.ldc + col) * 2u;
+          const uint32_t off = (uint32_t)(row * p.ldc + col) * ES;
           if (cvec) {
-            st_b64(make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3])), rc, n0 + col < N ? off : OOB);
+            if constexpr (DT == DT_F32)
+              st_b128(make_uint4(h[0], h[1], h[2], h[3]), rc, n0 + col < N ? off : OOB);
+            else
+              st_b64(make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3])), rc, n0 + col < N ? off : OOB);
           } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) st_b16(h[e], rc, n0 + col + e < N ? off + 2u * e : OOB);
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t oe = n0 + col + e < N ? off + ES * e : OOB;
+              if constexpr (DT == DT_F32) st_b32(h[e], rc, oe);
+              else st_b16(h[e], rc, oe);
+            }
           }
         }
     }
@@ -1002,9 +1062,9 @@ hipError_t launch_one(const KParams& kp, int batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, bool BF, int NS = 3>
+template <int BM, int BN, int WGM, int WGN, int BMODE, bool BVEC, int DT, int NS = 3>
 hipError_t launch_one3(const KParams& kp, int batch, hipStream_t s) {
-  auto fn = k_gemm3<BM, BN, WGM, WGN, BMODE, BVEC, BF, NS>;
+  auto fn = k_gemm3<BM, BN, WGM, WGN, BMODE, BVEC, DT, NS>;
   const size_t dyn = BMODE == B_CONV ? (size_t)conv_ktab_rows(kp.K) * sizeof(uint32_t) : 0;
   // static LDS: the stages and two bias buffers
   constexpr size_t stat = (size_t)NS * (BM + BN) * 64 * 2 + 2 * (BM > BN ? BM : BN) * 4;
@@ -1089,18 +1149,29 @@ bool use_v2() {
   return v == 1;
 }
 
+// Pipelined kernel (16-byte-aligned A); nullopt-style hipErrorNotSupported
+// when the tile has no pipelined instantiation.
+template <int BMODE, bool BVEC, int DT>
+hipError_t dispatch3(const Tile& t, const KParams& kp, int batch, hipStream_t s) {
+  const int w = t.wgm * t.wgn;
+  if (t.bm == 256 && t.bn == 128 && w == 8) return launch_one3<256, 128, 4, 2, BMODE, BVEC, DT>(kp, batch, s);
+  if (t.bm == 128 && t.bn == 256 && w == 8) return launch_one3<128, 256, 2, 4, BMODE, BVEC, DT>(kp, batch, s);
+  if (t.bm == 256 && t.bn == 128) return launch_one3<256, 128, 2, 2, BMODE, BVEC, DT>(kp, batch, s);
+  if (t.bm == 128 && t.bn == 256) return launch_one3<128, 256, 2, 2, BMODE, BVEC, DT>(kp, batch, s);
+  if (t.bm == 128 && t.bn == 128) return launch_one3<128, 128, 2, 2, BMODE, BVEC, DT>(kp, batch, s);
+  if (t.bm == 128 && t.bn == 64) return launch_one3<128, 64, 2, 2, BMODE, BVEC, DT>(kp, batch, s);
+  if (t.bm == 64 && t.bn == 64) return launch_one3<64, 64, 2, 2, BMODE, BVEC, DT>(kp, batch, s);
+  return hipErrorNotSupported;
+}
+
+// Register-staged kernel (16-bit types), also the path for unaligned A.
 template <int BMODE, bool AVEC, bool BVEC, bool BF>
 hipError_t dispatch_tile(const Tile& t, const KParams& kp, int batch, hipStream_t s) {
   const int w = t.wgm * t.wgn;
   if constexpr (AVEC) {
     if (!use_v2()) {
-      if (t.bm == 256 && t.bn == 128 && w == 8) return launch_one3<256, 128, 4, 2, BMODE, BVEC, BF>(kp, batch, s);
-      if (t.bm == 128 && t.bn == 256 && w == 8) return launch_one3<128, 256, 2, 4, BMODE, BVEC, BF>(kp, batch, s);
-      if (t.bm == 256 && t.bn == 128) return launch_one3<256, 128, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
-      if (t.bm == 128 && t.bn == 256) return launch_one3<128, 256, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
-      if (t.bm == 128 && t.bn == 128) return launch_one3<128, 128, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
-      if (t.bm == 128 && t.bn == 64) return launch_one3<128, 64, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
-      if (t.bm == 64 && t.bn == 64) return launch_one3<64, 64, 2, 2, BMODE, BVEC, BF>(kp, batch, s);
+      hipError_t e = dispatch3<BMODE, BVEC, BF ? DT_BF16 : DT_F16>(t, kp, batch, s);
+      if (e != hipErrorNotSupported) return e;
     }
   }
   if (t.bm == 256 && t.bn == 128 && w == 8) return launch_one<256, 128, 4, 2, BMODE, AVEC, BVEC, BF>(kp, batch, s);
@@ -1145,21 +1216,26 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
   // buffer offsets are 31-bit: a tile's rows of A / B, a slice's rows of a
   // [K,N] operand and one im2col input image must stay below 2 GiB
   if (d.lda >= (1LL << 22) || d.ldb >= (1LL << 22)) return hipErrorInvalidValue;
+  const bool f32 = d.dtype == WGX_FLOAT32;
+  const int es = f32 ? 4 : 2, epc = 16 / es;
   if (d.bmode == B_CONV) {
-    const long long img = (long long)d.K / (d.g.KH * d.g.KW) * d.g.IH * d.g.IW * 2;
+    const long long img = (long long)d.K / (d.g.KH * d.g.KW) * d.g.IH * d.g.IW * es;
     if (img >= (1LL << 31)) return hipErrorInvalidValue;
     kp.b_bytes = (uint32_t)img;
   }
   const bool bf = d.dtype == WGX_BFLOAT16;
   const auto aligned16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-  const bool avec = (d.K % 8 == 0) && (d.lda % 8 == 0) && (d.sA % 8 == 0) && aligned16(d.A);
+  const bool avec = (d.K % epc == 0) && (d.lda % epc == 0) && (d.sA % epc == 0) && aligned16(d.A);
   bool bvec;
   if (d.bmode == B_NK)
-    bvec = (d.K % 8 == 0) && (d.ldb % 8 == 0) && (d.sB % 8 == 0) && aligned16(d.B);
+    bvec = (d.K % epc == 0) && (d.ldb % epc == 0) && (d.sB % epc == 0) && aligned16(d.B);
   else if (d.bmode == B_KN)
-    bvec = (d.N % 8 == 0) && (d.ldb % 8 == 0) && (d.sB % 8 == 0) && aligned16(d.B);
+    bvec = (d.N % epc == 0) && (d.ldb % epc == 0) && (d.sB % epc == 0) && aligned16(d.B);
   else
     bvec = false;
+  // fp32 runs only on the pipelined kernel: A (and a [N,K] B) must be
+  // 16-byte vectors; the caller takes the vector-FMA kernel otherwise
+  if (f32 && (!avec || (d.bmode == B_NK && !bvec))) return hipErrorNotSupported;
   Tile t = choose_tile(d.M, d.N, d.K, d.batch, avec, d.bmode);
   if (d.bmode == B_NK && !bvec) t = {64, 64, 2, 2};
   if (d.bmode == B_KN && !bvec) t = {64, 64, 2, 2};
@@ -1168,12 +1244,19 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
   if (name) {
     char buf[96];
     static const char* modes[] = {"nk", "kn", "conv"};
-    snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw%d_%s%s%s", bf ? "bf16" : "f16", t.bm, t.bn,
-             t.wgm * t.wgn, modes[d.bmode], d.bmode == B_KN ? (knv ? "4x8" : "col") : "",
+    snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw%d_%s%s%s", f32 ? "f32" : (bf ? "bf16" : "f16"), t.bm,
+             t.bn, t.wgm * t.wgn, modes[d.bmode], d.bmode == B_KN ? (knv ? "4x8" : "col") : "",
              avec ? "" : "_scalarA");
     *name = buf;
   }
   if (bf && d.bmode == B_CONV) return hipErrorInvalidValue;  // bf16 convolution is not offered
+  if (f32) {
+    if (d.bmode == B_NK) return dispatch3<B_NK, true, DT_F32>(t, kp, d.batch, s);
+    if (d.bmode == B_KN)
+      return bvec ? dispatch3<B_KN, true, DT_F32>(t, kp, d.batch, s)
+                  : dispatch3<B_KN, false, DT_F32>(t, kp, d.batch, s);
+    return dispatch3<B_CONV, false, DT_F32>(t, kp, d.batch, s);
+  }
   if (!avec) {
     if (d.bmode == B_NK)
       return bf ? (bvec ? launch_one<64, 64, 2, 2, B_NK, false, true, true>(kp, d.batch, s)

@@ -372,13 +372,28 @@ int wgx_record_copy(wgx_ctx* c, void* dst, const void* src, uint64_t bytes) {
 
 // ------------------------------------------------------------------ GEMM family
 
+// float32 runs on the matrix cores (v_mfma_f32_32x32x2_f32, twice the rate
+// of unpacked vector FMA) when its operands are 16-byte vectors, else on the
+// LDS-blocked vector-FMA kernel; WGX_F32_VECTOR_FMA=1 forces the latter.
+static bool f32_on_mfma() {
+  static int v = -1;
+  if (v < 0) v = getenv("WGX_F32_VECTOR_FMA") ? 0 : 1;
+  return v == 1;
+}
+
 static int record_gemm(wgx_ctx* c, GemmDesc d) {
   std::string name;
-  hipError_t e = d.dtype == WGX_FLOAT32 ? launch_gemm_f32(d, c->dry(), &name)
-                                        : launch_gemm_mfma(d, c->dry(), &name);
+  bool mfma = d.dtype != WGX_FLOAT32;
+  hipError_t e;
+  if (d.dtype == WGX_FLOAT32 && f32_on_mfma()) {
+    e = launch_gemm_mfma(d, c->dry(), &name);
+    if (e == hipSuccess) mfma = true;
+    else if (e != hipErrorNotSupported) return c->hip_fail(e, "kernel set-up");
+  }
+  if (!mfma) e = launch_gemm_f32(d, c->dry(), &name);
+  else if (d.dtype != WGX_FLOAT32) e = launch_gemm_mfma(d, c->dry(), &name);
   if (e != hipSuccess) return c->hip_fail(e, "kernel set-up");
-  if (d.dtype == WGX_FLOAT32)
-    return c->push([d](hipStream_t s) { return launch_gemm_f32(d, s, nullptr); }, name);
+  if (!mfma) return c->push([d](hipStream_t s) { return launch_gemm_f32(d, s, nullptr); }, name);
   return c->push([d](hipStream_t s) { return launch_gemm_mfma(d, s, nullptr); }, name);
 }
 
