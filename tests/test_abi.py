@@ -71,8 +71,10 @@ def test_mm_validation(hctx, pkg):
     a = hctx.tensor("float32", [4, 8])
     b = hctx.tensor("float32", [8, 5])
     o = hctx.tensor("float32", [4, 5])
-    hctx.mm(a, b, o)
-    assert hctx.last_kernel.startswith("gemm_f32")
+    hctx.mm(a, b, o)  # K = 8: 16-byte rows, so float32 runs on the matrix cores
+    assert hctx.last_kernel.startswith("gemm_mfma_f32")
+    hctx.mm(hctx.tensor("float32", [4, 7]), hctx.tensor("float32", [7, 5]), o)
+    assert hctx.last_kernel.startswith("gemm_f32")  # K = 7: the vector-FMA kernel
     with pytest.raises(E, match="inner dimensions must match"):
         hctx.mm(a, a, o)
     with pytest.raises(E, match="Output shape|output shape"):
