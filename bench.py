@@ -22,6 +22,7 @@ host's cores on a bounded sample of the same workload.
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -58,7 +59,7 @@ def log(*a):
 
 
 # ---------------------------------------------------------------- builders
-def build_conv(ctx, I, c, dtype, seed, bias=True, batch=1):
+def build_conv(ctx, I, c, dtype, seed, bias=True, batch=1, repeat=1):
     xs = (batch,) + tuple(c["x"][1:])
     ys = [batch] + list(c["y"][1:])
     x = I.uniform(seed, xs, -1, 1)
@@ -67,8 +68,92 @@ def build_conv(ctx, I, c, dtype, seed, bias=True, batch=1):
     tb = ctx.from_numpy(I.uniform(seed + 2, (c["w"][0],), -0.1, 0.1), dtype) if bias else None
     ty = ctx.tensor(dtype, ys)
     groups = c.get("groups", 1)
-    ctx.convolution(tx, tw, tb, list(c["s"]), list(c["p"]), [1, 1], False, [0, 0], groups, ty)
+    for _ in range(repeat):
+        ctx.convolution(tx, tw, tb, list(c["s"]), list(c["p"]), [1, 1], False, [0, 0], groups, ty)
     return ctx.last_kernel
+
+
+# ---------------------------------------------------------------- HBM traffic
+COPY_BYTES = 512 << 20
+PROBE_REPS = 5
+
+
+def traffic_probe(W, I, v):
+    """Child run counted by rocprofv3: the headline's conv `v` (float32)
+    PROBE_REPS times, then a device copy of COPY_BYTES PROBE_REPS times (the
+    calibration)."""
+    ctx = W.Context(0)
+    try:
+        build_conv(ctx, I, CONV2[v], "float32", 40)
+        ctx.set_graph_mode(False)
+        for _ in range(PROBE_REPS):
+            ctx.submit()
+        ctx.sync()
+        ctx.reset()
+        src = ctx.tensor("float32", [COPY_BYTES // 4])
+        dst = ctx.tensor("float32", [COPY_BYTES // 4])
+        ctx.copy(src, dst)
+        for _ in range(PROBE_REPS):
+            ctx.submit()
+        ctx.sync()
+    finally:
+        ctx.destroy()
+
+
+def measure_traffic(v):
+    """HBM bytes per step of the headline conv `v` (its GEMM dispatch plus the
+    split-K reduction when there is one) from two rocprofv3 --pmc runs
+    (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by what the
+    counter reads for a plain copy of COPY_BYTES (which moves exactly
+    COPY_BYTES in each direction).  The copy's reading is the sum over the
+    blit dispatches issued after the last conv dispatch (the data uploads
+    before the conv are blits too), divided by PROBE_REPS."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None
+    res = {}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="wgx_pmc_", dir="/tmp")
+        try:
+            cmd = ["timeout", "-s", "KILL", "90", prof, "--pmc", counter, "-d", d, "-o", "run",
+                   "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__),
+                   "--traffic-probe", v]
+            r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True, timeout=120)
+            files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+            if r.returncode != 0 or not files:
+                log(f"traffic: rocprofv3 {counter} failed (rc {r.returncode})")
+                return None
+            rows = []
+            with open(files[0]) as f:
+                for row in csv.DictReader(f):
+                    if row["Counter_Name"] == counter:
+                        rows.append((int(row["Dispatch_Id"]), row["Kernel_Name"],
+                                     float(row["Counter_Value"])))
+            rows.sort()
+            conv = [(i, x) for i, n, x in rows
+                    if "k_gemm" in n or "k_sgemm" in n or "k_splitk" in n]
+            last = max((i for i, _ in conv), default=None)
+            copy = [x for i, n, x in rows if "copyBuffer" in n and last is not None and i > last]
+            if not conv or not copy:
+                log(f"traffic: no {counter} rows for the conv or the copy")
+                return None
+            res[counter] = (sum(x for _, x in conv) / PROBE_REPS, sum(copy) / PROBE_REPS)
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
+    f_k, f_c = res["FETCH_SIZE"]
+    w_k, w_c = res["WRITE_SIZE"]
+    fs, ws = COPY_BYTES / (f_c * 1024.0), COPY_BYTES / (w_c * 1024.0)
+    return {"bytes": int(f_k * 1024 * fs + w_k * 1024 * ws),
+            "fetch_kib": round(f_k, 1), "write_kib": round(w_k, 1),
+            "copy_fetch_kib": round(f_c, 1), "copy_write_kib": round(w_c, 1),
+            "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
 
 
 def time_ctx(ctx, reps, warm=3):
@@ -284,6 +369,9 @@ def main():
     ap.add_argument("--no-detail", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE_SIZE runs")
+    ap.add_argument("--traffic-probe", choices=list(CONV2), default=None,
+                    help=argparse.SUPPRESS)  # the child run that rocprofv3 counts
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on exactly one GPU (the hot path is not sharded); "
@@ -294,6 +382,9 @@ def main():
 
     pkg = load_package()
     W, I = pkg.wgx, pkg.inputs
+    if args.traffic_probe:
+        traffic_probe(W, I, args.traffic_probe)
+        return
 
     # ---- headline: config 2 (2a + 2b), float32, one submit per step
     ctx = W.Context(0)
@@ -313,22 +404,32 @@ def main():
     step_flops = sum(conv_flops(c) for c in CONV2.values())
     value = step_flops / (ms_step * 1e-3) / 1e9
 
-    # ---- dominant kernel: per-launch duration with HIP events on its stream
+    # ---- dominant kernel: average launch duration, HIP events recorded on the
+    # context's own stream around one submit of a graph holding REPS launches
+    # of the kernel (the same buffers each time)
     per_kernel = {}
+    reps_in_graph = 20
     for v, c in CONV2.items():
         kctx = W.Context(0)
         try:
-            build_conv(kctx, I, c, "float32", 40)
-            per_kernel[v] = time_ctx(kctx, 200)
+            build_conv(kctx, I, c, "float32", 40, repeat=reps_in_graph)
+            per_kernel[v] = time_ctx(kctx, 20) / reps_in_graph
         finally:
             kctx.destroy()
     dom = max(per_kernel, key=per_kernel.get)
     dom_ms = per_kernel[dom]
     achieved = conv_flops(CONV2[dom]) / (dom_ms * 1e-3) / 1e12
+    traffic = None if args.no_traffic else measure_traffic(dom)
     roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK["fp32_TFLOPs"],
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK["fp32_TFLOPs"], 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK["fp32_TFLOPs"], 4),
+                "traffic": traffic["bytes"] if traffic else None,
                 "kernel": kernels[dom], "workload": f"conv {dom}",
-                "launch_us": round(dom_ms * 1e3, 2)}
+                "launch_us": round(dom_ms * 1e3, 2),
+                "launch_covers": ("GEMM dispatch + split-K reduction dispatch"
+                                  if re.search(r"_k\d+$", kernels[dom]) else "GEMM dispatch"),
+                "algorithmic_bytes": conv_bytes(CONV2[dom], 4)}
+    if traffic:
+        roofline["traffic_detail"] = traffic
 
     detail = {}
     if not args.no_detail:

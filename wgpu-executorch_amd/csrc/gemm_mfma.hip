@@ -67,6 +67,8 @@ struct KParams {
   int gm;            // m-tiles per group of the tile order
   uint32_t b_bytes;  // B_CONV: bytes of one input image
   int batch;
+  int splits, kchunk;  // split-K: K ranges per tile, K slices per range
+  float* ws;           // split-K partial sums, [splits][batch][M][N]
 };
 
 template <bool BF>
@@ -667,6 +669,8 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_mn = tiles_m * p.tiles_n;
   const int ntiles = tiles_mn * p.batch;
+  const int S = p.splits;      // K ranges per tile (split-K)
+  const int nunits = ntiles * S;
   const int G = gridDim.x;
   const int rb = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
   const char* Ab = reinterpret_cast<const char*>(p.A);
@@ -694,13 +698,19 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
   struct TileState {
     rsrc_t ra, rb;
     int m0, n0, z, gn_col, colbase;
+    int tile, sp, kbase, kts;  // output tile, K range, its first k and slice count
     unsigned long long cmask;
     uint32_t bias_h;
   };
   const int nl = tid % BN;
   const int krun = tid / BN;
-  auto tile_state = [&](int tile) {
+  auto tile_state = [&](int unit) {
     TileState s;
+    const int tile = unit / S;
+    s.tile = tile;
+    s.sp = unit - tile * S;
+    s.kbase = s.sp * p.kchunk * BK;
+    s.kts = min(p.kchunk, KT - s.sp * p.kchunk);
     const int z = tile / tiles_mn, r = tile % tiles_mn;
     const int gsz = p.gm * p.tiles_n;
     const int grp = r / gsz, rr = r - grp * gsz;
@@ -893,25 +903,26 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     }
   };
 
-  int tile = rb;
-  if (tile >= ntiles) return;
-  TileState cur = tile_state(tile);
+  int unit = rb;
+  if (unit >= nunits) return;
+  TileState cur = tile_state(unit);
   BRegs RB;
 
   // the first NS-1 slices of a tile: DMA into stages 0..NS-2; register-staged
   // B slice 0 goes to LDS at the top of the tile loop, slice 1 in step 0
   auto prologue = [&](const TileState& st) {
-    if constexpr (!BDMA) load_b(st, 0, RB);
-    dma_rows(st.ra, p.lda, 0, stA(std::integral_constant<int, 0>{}), std::integral_constant<int, CHA>{});
+    const int k0 = st.kbase;
+    if constexpr (!BDMA) load_b(st, k0, RB);
+    dma_rows(st.ra, p.lda, k0, stA(std::integral_constant<int, 0>{}), std::integral_constant<int, CHA>{});
     if constexpr (BDMA)
-      dma_rows(st.rb, p.ldb, 0, stB(std::integral_constant<int, 0>{}), std::integral_constant<int, CHB>{});
-    dma_rows(st.ra, p.lda, BK, stA(std::integral_constant<int, 1>{}), std::integral_constant<int, CHA>{});
+      dma_rows(st.rb, p.ldb, k0, stB(std::integral_constant<int, 0>{}), std::integral_constant<int, CHB>{});
+    dma_rows(st.ra, p.lda, k0 + BK, stA(std::integral_constant<int, 1>{}), std::integral_constant<int, CHA>{});
     if constexpr (BDMA)
-      dma_rows(st.rb, p.ldb, BK, stB(std::integral_constant<int, 1>{}), std::integral_constant<int, CHB>{});
+      dma_rows(st.rb, p.ldb, k0 + BK, stB(std::integral_constant<int, 1>{}), std::integral_constant<int, CHB>{});
     if constexpr (NS > 3) {
-      dma_rows(st.ra, p.lda, 2 * BK, stA(std::integral_constant<int, 2>{}), std::integral_constant<int, CHA>{});
+      dma_rows(st.ra, p.lda, k0 + 2 * BK, stA(std::integral_constant<int, 2>{}), std::integral_constant<int, CHA>{});
       if constexpr (BDMA)
-        dma_rows(st.rb, p.ldb, 2 * BK, stB(std::integral_constant<int, 2>{}), std::integral_constant<int, CHB>{});
+        dma_rows(st.rb, p.ldb, k0 + 2 * BK, stB(std::integral_constant<int, 2>{}), std::integral_constant<int, CHB>{});
     }
   };
 
@@ -923,9 +934,12 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     constexpr int S1 = (S + 1) % NS, SL = (S + NS - 1) % NS;
     using I1 = std::integral_constant<int, S1>;
     using IL = std::integral_constant<int, SL>;
-    if constexpr (!BDMA) load_b(cur, (t + 1) * BK, RB);
-    dma_rows(cur.ra, p.lda, (t + NS - 1) * BK, stA(IL{}), std::integral_constant<int, CHA>{});
-    if constexpr (BDMA) dma_rows(cur.rb, p.ldb, (t + NS - 1) * BK, stB(IL{}), std::integral_constant<int, CHB>{});
+    // slices past this unit's K range (the next range's, or past K: zeros)
+    // are loaded but never multiplied
+    if constexpr (!BDMA) load_b(cur, cur.kbase + (t + 1) * BK, RB);
+    dma_rows(cur.ra, p.lda, cur.kbase + (t + NS - 1) * BK, stA(IL{}), std::integral_constant<int, CHA>{});
+    if constexpr (BDMA)
+      dma_rows(cur.rb, p.ldb, cur.kbase + (t + NS - 1) * BK, stB(IL{}), std::integral_constant<int, CHB>{});
     compute(stA(s_tag), stB(s_tag));
     if constexpr (!BDMA) store_b(stB(I1{}), RB);
     wait_vm<(NS - 2) * DMAS>();  // slice t+1 landed, the later ones may still run
@@ -934,7 +948,7 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
 
   prologue(cur);
   while (true) {
-    const int par = (tile / G) & 1;  // bias buffer of this tile
+    const int par = (unit / G) & 1;  // bias buffer of this unit
     if constexpr (!BDMA) store_b(stB(std::integral_constant<int, 0>{}), RB);
     if (p.bias_mode != BIAS_NONE && tid < BMAX) sbias[par][tid] = p.beta * to_f32<DT>(cur.bias_h);
 #pragma unroll
@@ -946,23 +960,55 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     wait_vm<(NS - 2) * DMAS>();  // slice 0 landed (slices 1.. may still run)
     __syncthreads();
 
-    for (int t = 0; t < KT; t += NS) {
+    const int kts = cur.kts;
+    for (int t = 0; t < kts; t += NS) {
       step(t, std::integral_constant<int, 0>{});
-      if (t + 1 < KT) step(t + 1, std::integral_constant<int, 1>{});
-      if (t + 2 < KT) step(t + 2, std::integral_constant<int, 2>{});
+      if (t + 1 < kts) step(t + 1, std::integral_constant<int, 1>{});
+      if (t + 2 < kts) step(t + 2, std::integral_constant<int, 2>{});
       if constexpr (NS > 3)
-        if (t + 3 < KT) step(t + 3, std::integral_constant<int, 3 % NS>{});
+        if (t + 3 < kts) step(t + 3, std::integral_constant<int, 3 % NS>{});
     }
     // the DMAs of the slices past K (zeros) land before the stages are
     // refilled for the next tile
     wait_vm<0>();
     __syncthreads();
 
-    const int m0 = cur.m0, n0 = cur.n0, z = cur.z;
-    const int next = tile + G;
-    if (next < ntiles) {  // the next tile's first slices run under this epilogue
+    const int m0 = cur.m0, n0 = cur.n0, z = cur.z, tile = cur.tile, sp = cur.sp;
+    const int next = unit + G;
+    if (next < nunits) {  // the next unit's first slices run under this epilogue
       cur = tile_state(next);
       prologue(cur);
+    }
+
+    // split-K: this unit's partial sum (fp32) goes to slab sp of the
+    // workspace, laid out like C ([batch][M][N], dense); the reduction kernel
+    // sums the slabs in order and runs the epilogue.
+    if (S > 1) {
+      const int mrows = min(BM, M - m0);
+      const rsrc_t rw = make_rsrc(p.ws + (((long long)sp * p.batch + z) * M + m0) * (long long)N + n0,
+                                  (uint32_t)((mrows - 1) * N + (N - n0)) * 4u);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int row = wm * WM + i * 32 + frow;
+            const int col = wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+            const uint32_t off = (uint32_t)(row * N + col) * 4u;
+            if ((N & 3) == 0) {
+              st_b128(make_uint4(__float_as_uint(acc[i][j][4 * g]), __float_as_uint(acc[i][j][4 * g + 1]),
+                                 __float_as_uint(acc[i][j][4 * g + 2]), __float_as_uint(acc[i][j][4 * g + 3])),
+                      rw, n0 + col < N ? off : OOB);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                st_b32(__float_as_uint(acc[i][j][4 * g + e]), rw, n0 + col + e < N ? off + 4u * e : OOB);
+            }
+          }
+      if (next >= nunits) break;
+      unit = next;
+      continue;
     }
 
     // ------------------------------------------------------ epilogue
@@ -1009,8 +1055,50 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
           }
         }
     }
-    if (next >= ntiles) break;
-    tile = next;
+    if (next >= nunits) break;
+    unit = next;
+  }
+}
+
+// Split-K reduction: C = epilogue(sum over ranges of ws[r]), the ranges
+// summed in order 0..splits-1 so the result does not depend on scheduling.
+// One thread per 4 consecutive outputs of a row.
+template <int DT>
+__global__ __launch_bounds__(256) void k_splitk_reduce(KParams p) {
+  const int M = p.M, N = p.N, S = p.splits;
+  const int nq = (N + 3) / 4;
+  const long long total = (long long)p.batch * M * nq;
+  const long long slab = (long long)p.batch * M * N;
+  char* Cb = reinterpret_cast<char*>(p.C);
+  constexpr int ES = DT == DT_F32 ? 4 : 2;
+  for (long long q = (long long)blockIdx.x * 256 + threadIdx.x; q < total; q += (long long)gridDim.x * 256) {
+    const int n = (int)(q % nq) * 4;
+    const long long zm = q / nq;
+    const int m = (int)(zm % M), z = (int)(zm / M);
+    const long long base = zm * N + n;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < S; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) v[e] += p.ws[(long long)r * slab + base + e];
+    const long long cbase = (long long)z * p.sC + (long long)m * p.ldc + n;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (n + e >= N) continue;
+      float x = p.alpha * v[e];
+      if (p.bias_mode == BIAS_ROW) {
+        x += p.beta * (DT == DT_F32 ? reinterpret_cast<const float*>(p.bias)[m] : ld_f32<DT == DT_BF16>(p.bias[m]));
+      } else if (p.bias_mode == BIAS_COL) {
+        x += p.beta *
+             (DT == DT_F32 ? reinterpret_cast<const float*>(p.bias)[n + e] : ld_f32<DT == DT_BF16>(p.bias[n + e]));
+      }
+      if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+      if constexpr (DT == DT_F32)
+        reinterpret_cast<float*>(Cb)[cbase + e] = x;
+      else
+        reinterpret_cast<uint16_t*>(Cb)[cbase + e] = st_bits<DT == DT_BF16>(x);
+    }
+    (void)ES;
   }
 }
 
@@ -1083,13 +1171,13 @@ hipError_t launch_one3(const KParams& kp, int batch, hipStream_t s) {
     per_cu = 1;
   const long long ntiles = (long long)((kp.M + BM - 1) / BM) * kp.tiles_n * batch;
   long long grid = (long long)device_cus() * per_cu;
-  if (grid > ntiles) grid = ntiles;
+  if (grid > ntiles * kp.splits) grid = ntiles * kp.splits;
   KParams k2 = kp;
   k2.batch = batch;
   {
     const int tiles_m = (kp.M + BM - 1) / BM;
-    const double per_xcd = (double)(grid < 8 ? 1 : grid / 8);
-    int gm = (int)lround(sqrt(per_xcd * BN / BM));
+    const double per_xcd = (double)(grid < 8 ? 1 : grid / 8) / kp.splits;
+    int gm = (int)lround(sqrt((per_xcd < 1 ? 1 : per_xcd) * BN / BM));
     k2.gm = gm < 1 ? 1 : (gm > tiles_m ? tiles_m : gm);
   }
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WGM * WGN * 64), dyn, s, k2);
@@ -1188,6 +1276,65 @@ hipError_t dispatch_tile(const Tile& t, const KParams& kp, int batch, hipStream_
 
 }  // namespace
 
+namespace {
+
+// What launch_gemm_mfma decides from the shapes alone.
+struct Plan {
+  bool f32, bf, avec, bvec;
+  int es;
+  Tile t;
+  bool pipelined;  // runs k_gemm3 (split-K capable)
+};
+
+Plan make_plan(const GemmDesc& d) {
+  Plan pl;
+  pl.f32 = d.dtype == WGX_FLOAT32;
+  pl.bf = d.dtype == WGX_BFLOAT16;
+  pl.es = pl.f32 ? 4 : 2;
+  const int epc = 16 / pl.es;
+  const auto aligned16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  pl.avec = (d.K % epc == 0) && (d.lda % epc == 0) && (d.sA % epc == 0) && aligned16(d.A);
+  if (d.bmode == B_NK)
+    pl.bvec = (d.K % epc == 0) && (d.ldb % epc == 0) && (d.sB % epc == 0) && aligned16(d.B);
+  else if (d.bmode == B_KN)
+    pl.bvec = (d.N % epc == 0) && (d.ldb % epc == 0) && (d.sB % epc == 0) && aligned16(d.B);
+  else
+    pl.bvec = false;
+  pl.t = choose_tile(d.M, d.N, d.K, d.batch, pl.avec, d.bmode);
+  if (d.bmode != B_CONV && !pl.bvec) pl.t = {64, 64, 2, 2};
+  if (pl.f32)
+    pl.pipelined = pl.avec && (d.bmode != B_NK || pl.bvec);
+  else
+    pl.pipelined = pl.avec && pl.bvec == (d.bmode != B_CONV) && !use_v2() &&
+                   !(pl.t.bm == 256 && pl.t.bn == 256);
+  if (pl.bf && d.bmode == B_CONV) pl.pipelined = false;
+  return pl;
+}
+
+}  // namespace
+
+// Split K when the tiles alone leave CUs idle: the number of ranges that
+// brings the units nearest to one per CU (so 200 tiles on 256 CUs stay
+// whole, 100 tiles become 300 units), each range at least 8 K slices long,
+// at most 8 ranges.
+int gemm_split_plan(const GemmDesc& d, size_t* ws_bytes) {
+  *ws_bytes = 0;
+  const Plan pl = make_plan(d);
+  if (!pl.pipelined) return 1;
+  const long long ntiles =
+      (long long)((d.M + pl.t.bm - 1) / pl.t.bm) * ((d.N + pl.t.bn - 1) / pl.t.bn) * d.batch;
+  const int kt = (d.K + 128 / pl.es - 1) / (128 / pl.es);
+  int splits = (int)((device_cus() + ntiles / 2) / ntiles);
+  if (splits > kt / 8) splits = kt / 8;
+  if (splits > 8) splits = 8;
+  if (splits < 2) return 1;
+  const int kchunk = (kt + splits - 1) / splits;
+  splits = (kt + kchunk - 1) / kchunk;  // no empty range
+  if (splits < 2) return 1;
+  *ws_bytes = (size_t)splits * d.batch * d.M * d.N * sizeof(float);
+  return splits;
+}
+
 hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name) {
   KParams kp;
   kp.A = static_cast<const uint16_t*>(d.A);
@@ -1216,40 +1363,69 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
   // buffer offsets are 31-bit: a tile's rows of A / B, a slice's rows of a
   // [K,N] operand and one im2col input image must stay below 2 GiB
   if (d.lda >= (1LL << 22) || d.ldb >= (1LL << 22)) return hipErrorInvalidValue;
-  const bool f32 = d.dtype == WGX_FLOAT32;
-  const int es = f32 ? 4 : 2, epc = 16 / es;
+  const Plan pl = make_plan(d);
+  const bool f32 = pl.f32, bf = pl.bf, avec = pl.avec, bvec = pl.bvec;
+  const int es = pl.es;
+  const Tile t = pl.t;
   if (d.bmode == B_CONV) {
     const long long img = (long long)d.K / (d.g.KH * d.g.KW) * d.g.IH * d.g.IW * es;
     if (img >= (1LL << 31)) return hipErrorInvalidValue;
     kp.b_bytes = (uint32_t)img;
   }
-  const bool bf = d.dtype == WGX_BFLOAT16;
-  const auto aligned16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-  const bool avec = (d.K % epc == 0) && (d.lda % epc == 0) && (d.sA % epc == 0) && aligned16(d.A);
-  bool bvec;
-  if (d.bmode == B_NK)
-    bvec = (d.K % epc == 0) && (d.ldb % epc == 0) && (d.sB % epc == 0) && aligned16(d.B);
-  else if (d.bmode == B_KN)
-    bvec = (d.N % epc == 0) && (d.ldb % epc == 0) && (d.sB % epc == 0) && aligned16(d.B);
-  else
-    bvec = false;
   // fp32 runs only on the pipelined kernel: A (and a [N,K] B) must be
   // 16-byte vectors; the caller takes the vector-FMA kernel otherwise
-  if (f32 && (!avec || (d.bmode == B_NK && !bvec))) return hipErrorNotSupported;
-  Tile t = choose_tile(d.M, d.N, d.K, d.batch, avec, d.bmode);
-  if (d.bmode == B_NK && !bvec) t = {64, 64, 2, 2};
-  if (d.bmode == B_KN && !bvec) t = {64, 64, 2, 2};
+  if (f32 && !pl.pipelined) return hipErrorNotSupported;
   kp.tiles_n = (d.N + t.bn - 1) / t.bn;
+  kp.splits = 1;
+  kp.kchunk = 1 << 30;
+  kp.ws = nullptr;
+  if (d.splits > 1) {
+    if (!pl.pipelined || !d.ws) return hipErrorInvalidValue;
+    const int kt = (d.K + 128 / es - 1) / (128 / es);
+    kp.splits = d.splits;
+    kp.kchunk = (kt + d.splits - 1) / d.splits;
+    kp.ws = d.ws;
+  }
   const bool knv = d.bmode == B_KN && bvec;
   if (name) {
     char buf[96];
     static const char* modes[] = {"nk", "kn", "conv"};
-    snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw%d_%s%s%s", f32 ? "f32" : (bf ? "bf16" : "f16"), t.bm,
+    char split[16] = "";
+    if (kp.splits > 1) snprintf(split, sizeof split, "_k%d", kp.splits);
+    snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw%d_%s%s%s%s", f32 ? "f32" : (bf ? "bf16" : "f16"), t.bm,
              t.bn, t.wgm * t.wgn, modes[d.bmode], d.bmode == B_KN ? (knv ? "4x8" : "col") : "",
-             avec ? "" : "_scalarA");
+             avec ? "" : "_scalarA", split);
     *name = buf;
   }
   if (bf && d.bmode == B_CONV) return hipErrorInvalidValue;  // bf16 convolution is not offered
+  if (kp.splits > 1) {
+    // split-K: the GEMM writes per-range partial sums, a second kernel reduces
+    hipError_t e;
+    const int dt = f32 ? DT_F32 : (bf ? DT_BF16 : DT_F16);
+    if (dt == DT_F32) {
+      e = d.bmode == B_NK ? dispatch3<B_NK, true, DT_F32>(t, kp, d.batch, s)
+          : d.bmode == B_KN ? (bvec ? dispatch3<B_KN, true, DT_F32>(t, kp, d.batch, s)
+                                    : dispatch3<B_KN, false, DT_F32>(t, kp, d.batch, s))
+                            : dispatch3<B_CONV, false, DT_F32>(t, kp, d.batch, s);
+    } else if (dt == DT_BF16) {
+      e = d.bmode == B_NK ? dispatch3<B_NK, true, DT_BF16>(t, kp, d.batch, s)
+                          : dispatch3<B_KN, true, DT_BF16>(t, kp, d.batch, s);
+    } else {
+      e = d.bmode == B_NK ? dispatch3<B_NK, true, DT_F16>(t, kp, d.batch, s)
+          : d.bmode == B_KN ? dispatch3<B_KN, true, DT_F16>(t, kp, d.batch, s)
+                            : dispatch3<B_CONV, false, DT_F16>(t, kp, d.batch, s);
+    }
+    if (e != hipSuccess || is_dry(s)) return e;
+    KParams kr = kp;
+    kr.batch = d.batch;
+    const long long total = (long long)d.batch * d.M * ((d.N + 3) / 4);
+    long long grid = (total + 255) / 256;
+    if (grid > 4LL * device_cus()) grid = 4LL * device_cus();
+    if (dt == DT_F32) hipLaunchKernelGGL(k_splitk_reduce<DT_F32>, dim3((unsigned)grid), dim3(256), 0, s, kr);
+    else if (dt == DT_BF16) hipLaunchKernelGGL(k_splitk_reduce<DT_BF16>, dim3((unsigned)grid), dim3(256), 0, s, kr);
+    else hipLaunchKernelGGL(k_splitk_reduce<DT_F16>, dim3((unsigned)grid), dim3(256), 0, s, kr);
+    return hipGetLastError();
+  }
   if (f32) {
     if (d.bmode == B_NK) return dispatch3<B_NK, true, DT_F32>(t, kp, d.batch, s);
     if (d.bmode == B_KN)

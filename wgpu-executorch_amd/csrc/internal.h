@@ -51,7 +51,15 @@ struct GemmDesc {
   int bmode;
   ConvGeom g;
   const uint32_t* ktab;  // device table for B_CONV: Kpad entries (off << 6) | tap
+  // split-K (set from gemm_split_plan): splits > 1 divides K into that many
+  // contiguous ranges; ws holds their fp32 partial sums, [splits][batch][M][N]
+  int splits;
+  float* ws;
 };
+
+// Split-K plan for an MFMA launch: how many K ranges (1 = none) and the
+// workspace size the launch then needs.
+int gemm_split_plan(const GemmDesc& d, size_t* ws_bytes);
 
 // Table rows needed for a B_CONV launch (K rounded up to the largest K tile).
 int conv_ktab_rows(int K);

@@ -384,14 +384,25 @@ static bool f32_on_mfma() {
 static int record_gemm(wgx_ctx* c, GemmDesc d) {
   std::string name;
   bool mfma = d.dtype != WGX_FLOAT32;
-  hipError_t e;
+  hipError_t e = hipSuccess;
+  d.splits = 1;
   if (d.dtype == WGX_FLOAT32 && f32_on_mfma()) {
     e = launch_gemm_mfma(d, c->dry(), &name);
     if (e == hipSuccess) mfma = true;
     else if (e != hipErrorNotSupported) return c->hip_fail(e, "kernel set-up");
   }
+  if (mfma) {
+    // split-K: the partial-sum workspace is owned by the context
+    size_t ws_bytes = 0;
+    const int splits = gemm_split_plan(d, &ws_bytes);
+    if (splits > 1) {
+      d.ws = static_cast<float*>(c->owned_alloc(ws_bytes));
+      if (!d.ws) return c->fail(WGX_ERR_OOM, "gemm: split-K workspace allocation failed");
+      d.splits = splits;
+    }
+  }
   if (!mfma) e = launch_gemm_f32(d, c->dry(), &name);
-  else if (d.dtype != WGX_FLOAT32) e = launch_gemm_mfma(d, c->dry(), &name);
+  else e = launch_gemm_mfma(d, c->dry(), &name);
   if (e != hipSuccess) return c->hip_fail(e, "kernel set-up");
   if (!mfma) return c->push([d](hipStream_t s) { return launch_gemm_f32(d, s, nullptr); }, name);
   return c->push([d](hipStream_t s) { return launch_gemm_mfma(d, s, nullptr); }, name);
