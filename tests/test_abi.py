@@ -119,8 +119,14 @@ def test_conv_validation_and_variants(hctx, pkg):
     # 100 output tiles for 256 CUs: K = 1152 is split into ranges (suffix _k<ranges>)
     assert "_conv_k" in conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1))
     assert "_kn" in conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8])
-    assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3"
-    assert conv([1, 512, 20, 20], [512, 1, 5, 5], [1, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5"
+    assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3s1_r4v8"
+    assert conv([1, 512, 20, 20], [512, 1, 5, 5], [1, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5s2_r4v4"
+    # odd widths (and float32) take the LDS-tiled kernel of the same family
+    assert conv([1, 6, 13, 17], [6, 1, 3, 3], [1, 6, 13, 17], pad=(1, 1), groups=6) == "depthwise_f16_3x3s1_v4"
+    assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256,
+                dtype="float32") == "depthwise_f32_3x3s1_v8"
+    # dilation 2 is outside the fast family: the general depthwise kernel
+    assert conv([1, 8, 12, 12], [8, 1, 3, 3], [1, 8, 12, 12], pad=(2, 2), dil=(2, 2), groups=8) == "depthwise_f16_3x3"
     assert conv([1, 8, 10, 10], [12, 4, 3, 3], [1, 12, 10, 10], pad=(1, 1), groups=2) == "conv_grouped_direct"
     assert conv([1, 2, 3, 3], [2, 2, 3, 3], [1, 2, 6, 6], (2, 2), (1, 1), transposed=True, op=(1, 1)) == "conv_transpose_direct"
     assert conv([1, 3, 64, 64], [16, 3, 3, 3], [1, 16, 32, 32], (2, 2), (1, 1), dtype="float32").startswith("gemm_f32")

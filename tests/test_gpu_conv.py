@@ -84,6 +84,78 @@ def test_config3_depthwise_fp16(gpu_ctx, orc, pkg, case):
     assert normwise(got, emu) < 1e-2
 
 
+DW_SWEEP = [
+    # x shape, kernel, stride, clamp -- "same" padding (k // 2), dilation 1
+    ((2, 24, 40, 40), 3, 1, False),      # 8-wide segments, 16-byte rows
+    ((1, 8, 20, 20), 5, 2, False),       # 4-wide segments, rows straddle chunks
+    ((1, 6, 13, 17), 3, 1, True),        # odd width, clamp epilogue
+    ((1, 4, 15, 15), 3, 2, False),       # stride 2, odd size
+    ((1, 5, 9, 22), 5, 1, False),        # 5x5 stride 1
+    ((1, 3, 300, 300), 3, 1, False),     # bands of one large plane (last band short)
+    ((1, 2, 129, 131), 5, 2, True),      # bands, stride 2, odd sizes
+    ((1, 1537, 8, 8), 3, 1, False),      # several planes per block, partial last block
+    ((3, 7, 1, 1), 3, 1, False),         # 1x1 image: every tap but the centre is padding
+    ((1, 4, 8, 256), 3, 1, False),       # 32 segments per row
+    ((1, 3, 10, 512), 3, 1, True),       # 64 segments: one plane per wave
+    ((40, 256, 40, 40), 3, 1, False),    # enough waves for 8-row bands
+    ((84, 512, 20, 20), 5, 2, False),    # 8-row bands, stride 2, masked last segment
+]
+
+
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_depthwise_sweep(gpu_ctx, orc, pkg, dtype):
+    """Depthwise fast family (K x K, stride 1/2, same padding) against the fp64
+    oracle, including bands of large planes, several planes per block and the
+    clamp epilogue."""
+    I = pkg.inputs
+    for i, (xs, k, s, clamp) in enumerate(DW_SWEEP):
+        c = xs[1]
+        x = round_in(I.normal(1000 + i, xs), dtype)
+        w = round_in(I.uniform(1100 + i, (c, 1, k, k), -0.5, 0.5), dtype)
+        b = round_in(I.uniform(1200 + i, (c,), -0.5, 0.5), dtype)
+        p = (k // 2, k // 2)
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), p, groups=c)
+        cl = (-0.5, 0.75) if clamp else None
+        got, kernel = run_conv(gpu_ctx, x, w, b, dtype, (s, s), p, groups=c,
+                               out_shape=list(ref.shape), clamp=cl)
+        if cl:
+            ref = np.clip(ref, *cl)
+        assert kernel.startswith(f"depthwise_{ {'float16': 'f16', 'float32': 'f32'}[dtype] }"
+                                 f"_{k}x{k}s{s}"), kernel
+        assert_parity(got, ref, refa, dtype, k * k, f"dw {i} {dtype} {xs} k{k} s{s} {kernel}")
+
+
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_depthwise_unaligned_views(gpu_ctx, orc, pkg, dtype):
+    """Input and output views that start off a 16-byte boundary (program
+    memory-plan offsets can): the staging reads aligned chunks around the view
+    and the tail chunk of the input element-wise, stores fall back to scalar."""
+    I = pkg.inputs
+    es = 2 if dtype == "float16" else 4
+    xs, k = (1, 16, 24, 24), 3
+    x = round_in(I.normal(1300, xs), dtype)
+    w = round_in(I.uniform(1301, (16, 1, k, k), -0.5, 0.5), dtype)
+    ref, refa = orc.conv2d_f64(x, w, None, (1, 1), (1, 1), groups=16)
+    nx = int(np.prod(xs))
+    bx = gpu_ctx.storage_buffer(nx * es + 64)
+    by = gpu_ctx.storage_buffer(nx * es + 64)
+    for ox, oy in ((es, 3 * es), (7 * es, 0), (64 - 0, es)):
+        # the input view ends exactly at the end of its buffer when ox == 64
+        tx = gpu_ctx.tensor(dtype, list(xs), bx + ox)
+        tx.set_data(x.astype(np.float16) if dtype == "float16" else x.astype(np.float32))
+        tw = gpu_ctx.from_numpy(w, dtype)
+        ty = gpu_ctx.tensor(dtype, list(xs), by + oy)
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 16, ty)
+        kernel = gpu_ctx.last_kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        assert_parity(ty.get_f32(), ref, refa, dtype, 9, f"unaligned x+{ox} y+{oy} {kernel}")
+    gpu_ctx.reset()
+    gpu_ctx.free(bx)
+    gpu_ctx.free(by)
+
+
 CONV_SWEEP = [
     # x shape, w shape, stride, pad, dilation, groups
     ((1, 3, 64, 64), (16, 3, 3, 3), (2, 2), (1, 1), (1, 1), 1),      # stem: K = 27

@@ -3,19 +3,40 @@
 //
 // Serves the depthwise branch of aten.convolution (src/shaders/convolution/
 // index.ts:194-221: conv2d-depthwise-3x3*.wgsl.ts for 3x3 s1 p1 d1 and
-// conv2d-depthwise*.wgsl.ts for any other kernel <= 7x7).  One kernel covers
-// both: the work is HBM-bound (about 2 flop per byte), so the design goal is
-// to move every input and output byte once, with full-width coalesced accesses.
+// conv2d-depthwise*.wgsl.ts for any other kernel <= 7x7).  The work is
+// HBM-bound (about 2 flop per byte for 3x3 stride 1), so the design goal is to
+// move every input and output byte once, in full-width coalesced accesses,
+// while keeping the per-output instruction count well under what the vector
+// ALUs can issue at HBM speed (about 20 per output for fp16 3x3).
 //
-// A block owns a band of output rows of one plane (or several whole planes when
-// a plane has fewer outputs than the block has lanes).  It streams the input
-// rows the band needs into LDS once -- zero-filled outside the image, so the
-// stencil loop has no bounds tests -- then each lane produces outputs along a
-// row (consecutive lanes -> consecutive ow, so the stores coalesce).  Accumulation:
-// bias first, then taps kh-outer / kw-inner (the reference's order,
-// conv2d-depthwise.wgsl.ts:228-268), in float32, rounded once.
+// Three kernels, tried in this order:
+//  * k_dw_reg<K, S, OV, R> (fp16; K x K with K in {3, 5}, stride S in {1, 2}
+//    in both dimensions, "same" padding P = K/2, dilation 1, even widths): no
+//    LDS at all.  Each lane walks a band of R output rows down a column strip
+//    of OV outputs, holding every input row of the band in registers (packed
+//    halves), with the halo columns taken from the neighbouring lanes.  Tap
+//    pairs are v_dot2_f32_f16, odd taps v_fma_mix_f32: fp32 accumulation
+//    without unpacking the input.
+//  * k_dw_fast<DT, K, S, OV>: the same kernel family for any width and for
+//    float32.  A block owns ppb whole planes, or a band of output rows of one
+//    large plane.  The input rows it needs form one contiguous range of
+//    memory; the block reads it with 16-byte vector loads (aligned chunks of
+//    the flat range, so any plane width works) and writes it, converted to
+//    fp32, into an LDS tile with a zero border -- the stencil loop then has no
+//    bounds tests.  Each lane produces OV consecutive outputs of one row from
+//    float4 reads of its input window and writes them with one vector store;
+//    consecutive lanes own consecutive output segments, so stores coalesce.
+//  * k_depthwise<DT, KH, KW>: any kernel size, stride, padding and dilation
+//    (element-wise staging through LDS).  Correct for every shape the
+//    convolution driver accepts; used where the two above do not apply.
+// All three accumulate in fp32 in the reference's order: bias, then taps
+// kh-outer / kw-inner (conv2d-depthwise.wgsl.ts:228-268), rounded once.
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
+
+#include <algorithm>
+#include <type_traits>
 
 #include "internal.h"
 
@@ -50,16 +71,20 @@ __device__ __forceinline__ float ldv(const void* p, long long i) {
 }
 
 template <int DT>
+__device__ __forceinline__ uint32_t to_bits(float v) {
+  if constexpr (DT == WGX_FLOAT32) return __float_as_uint(v);
+  else if constexpr (DT == WGX_FLOAT16)
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
+  else {
+    const uint32_t u = __float_as_uint(v);
+    return ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  }
+}
+
+template <int DT>
 __device__ __forceinline__ void stv(void* p, long long i, float v) {
   if constexpr (DT == WGX_FLOAT32) static_cast<float*>(p)[i] = v;
-  else if constexpr (DT == WGX_FLOAT16)
-    static_cast<_Float16*>(p)[i] = (_Float16)v;
-  else {
-    uint32_t u = __float_as_uint(v);
-    uint16_t h = ((u & 0x7fffffffu) > 0x7f800000u) ? (uint16_t)((u >> 16) | 0x40u)
-                                                   : (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-    static_cast<uint16_t*>(p)[i] = h;
-  }
+  else static_cast<uint16_t*>(p)[i] = (uint16_t)to_bits<DT>(v);
 }
 
 template <int DT, int KH_, int KW_>
@@ -129,6 +154,571 @@ __global__ __launch_bounds__(NT) void k_depthwise(DwParams p) {
   }
 }
 
+// ------------------------------------------------------------ fast family
+// n / d for 0 <= n < 2^31 by a multiply-high and a shift (m, l from
+// make_fastdiv: l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1).
+struct FastDiv {
+  uint32_t m, l;
+};
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) { return (__umulhi(n, f.m) + n) >> f.l; }
+FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const unsigned long long m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+  return {(uint32_t)m, l};
+}
+
+struct DwFast {
+  const char* xa;    // x rounded down to 16 bytes
+  uint32_t lead0;    // elements of xa before x
+  unsigned long long x_end;  // bytes from xa to the end of x
+  const void* w;
+  const void* bias;
+  void* y;
+  int C, IH, IW, OH, OW;
+  int multi;  // 1: blocks of whole planes; 0: bands of one plane
+  int ppb, nplanes, toh, bands, segs;
+  int LW, LR, PLANE;  // LDS tile: row pitch, rows and plane stride in floats
+  FastDiv fd_plane;  // IH * IW
+  FastDiv fd_iw;     // IW
+  FastDiv fd_items;  // OH * segs (items of one whole plane)
+  FastDiv fd_segs;   // segs
+  int has_clamp;
+  float cmin, cmax;
+};
+
+__device__ __forceinline__ void unpack(const uint4& v, float* f, std::integral_constant<int, WGX_FLOAT32>) {
+  f[0] = __uint_as_float(v.x);
+  f[1] = __uint_as_float(v.y);
+  f[2] = __uint_as_float(v.z);
+  f[3] = __uint_as_float(v.w);
+}
+__device__ __forceinline__ void unpack(const uint4& v, float* f, std::integral_constant<int, WGX_FLOAT16>) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] & 0xffffu));
+    f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] >> 16));
+  }
+}
+__device__ __forceinline__ void unpack(const uint4& v, float* f, std::integral_constant<int, WGX_BFLOAT16>) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(u[i] << 16);
+    f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+
+template <int DT, int K, int S, int OV>
+__global__ __launch_bounds__(NT) void k_dw_fast(DwFast p) {
+  constexpr int ES = DT == WGX_FLOAT32 ? 4 : 2;
+  constexpr int EPC = 16 / ES;               // elements per 16-byte chunk
+  constexpr int P = K / 2;                   // "same" padding
+  constexpr int KK = K * K;
+  constexpr int WST = (KK + 1 + 3) / 4 * 4;  // LDS floats per plane: taps, bias, pad
+  constexpr int WN = (OV - 1) * S + K;       // input window of one kernel row
+  constexpr int NW4 = (WN + 3) / 4;          // ... read as float4s
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x;
+
+  int plane0, oh0, nloc, rows_here, rofs;
+  uint32_t nq;             // input elements this block stages
+  unsigned long long g0;   // first of them (flat index into x)
+  if (p.multi) {
+    plane0 = blockIdx.x * p.ppb;
+    nloc = min(p.ppb, p.nplanes - plane0);
+    oh0 = 0;
+    rows_here = p.OH;
+    rofs = P;  // LDS row of ih = 0
+    g0 = (unsigned long long)plane0 * p.IH * p.IW;
+    nq = (uint32_t)(nloc * p.IH * p.IW);
+  } else {
+    plane0 = blockIdx.x / p.bands;
+    const int band = blockIdx.x - plane0 * p.bands;
+    nloc = 1;
+    oh0 = band * p.toh;
+    rows_here = min(p.toh, p.OH - oh0);
+    const int ih_lo = oh0 * S - P;
+    const int r_s = max(ih_lo, 0), r_e = min(ih_lo + p.LR, p.IH);
+    rofs = r_s - ih_lo;
+    g0 = ((unsigned long long)plane0 * p.IH + r_s) * p.IW;
+    nq = r_e > r_s ? (uint32_t)((r_e - r_s) * p.IW) : 0u;
+  }
+  const int rows_st = p.multi ? p.IH : 0;  // staged rows per plane (multi only)
+  float* tile = lds;
+  float* wl = lds + p.ppb * p.PLANE;
+
+  // 1. zero the tile (its border is the zero padding); weights and bias
+  {
+    const int n4 = nloc * p.PLANE / 4;
+    float4* t4 = reinterpret_cast<float4*>(tile);
+    for (int i = tid; i < n4; i += NT) t4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = tid; i < nloc * WST; i += NT) {
+      const int pp = i / WST, j = i - pp * WST;
+      const int c = (plane0 + pp) % p.C;
+      float v = 0.0f;
+      if (j < KK) v = ldv<DT>(p.w, (long long)c * KK + j);
+      else if (j == KK && p.bias) v = ldv<DT>(p.bias, c);
+      wl[i] = v;
+    }
+  }
+  __syncthreads();
+
+  // 2. stage the input: 16-byte chunks of the flat range [g0, g0 + nq),
+  //    chunk k of the block starts at byte cb0 + 16 k from xa
+  if (nq > 0) {
+    const unsigned long long byte_lo = (g0 + p.lead0) * ES;
+    const unsigned long long cb0 = byte_lo & ~15ull;
+    const uint32_t lead = (uint32_t)(byte_lo - cb0) / ES;  // elements before g0 in chunk 0
+    const uint32_t nck = (uint32_t)((byte_lo + (unsigned long long)nq * ES - cb0 + 15) / 16);
+    const unsigned long long left = p.x_end - cb0;
+    const uint32_t rec = left > 0x7fffffffull ? 0x7fffffffu : (uint32_t)left;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p.xa + cb0), 0, (int)rec,
+                                                                        0x00020000);
+    const uint32_t plane_in = (uint32_t)(p.IH * p.IW);
+    for (uint32_t base = 0; base < nck; base += 4 * NT) {
+      uint4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t k = base + u * NT + tid;
+        // whole chunks inside x: one vector load; the tail chunk of x (which
+        // may end mid-chunk at the end of its allocation) goes element-wise
+        if (k < nck && 16u * k + 16u <= rec) {
+          const auto r = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(16u * k), 0, 0);
+          v[u] = make_uint4(r[0], r[1], r[2], r[3]);
+        } else if (k < nck) {
+          uint32_t e[EPC];
+#pragma unroll
+          for (int j = 0; j < EPC; ++j) {
+            const uint32_t off = 16u * k + ES * j;
+            e[j] = off + ES <= rec ? (ES == 4 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0)
+                                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0))
+                                   : 0u;
+          }
+          if constexpr (ES == 4) v[u] = make_uint4(e[0], e[1], e[2], e[3]);
+          else
+            v[u] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t k = base + u * NT + tid;
+        if (k >= nck) break;
+        float f[EPC];
+        unpack(v[u], f, std::integral_constant<int, DT>{});
+        const uint32_t j0 = k == 0 ? lead : 0u;
+        const uint32_t q0 = k * EPC + j0 - lead;  // first element of the chunk inside the range
+        uint32_t pp = p.multi ? fdiv(q0, p.fd_plane) : 0u;
+        const uint32_t rem = q0 - pp * plane_in;
+        uint32_t r = fdiv(rem, p.fd_iw);
+        uint32_t col = rem - r * p.IW;
+        uint32_t li = pp * p.PLANE + (r + rofs) * p.LW + P + col;
+        if (j0 == 0 && q0 + EPC <= nq && col + EPC <= (uint32_t)p.IW) {
+#pragma unroll
+          for (int j = 0; j < EPC; ++j) tile[li + j] = f[j];
+        } else {
+#pragma unroll
+          for (int j = 0; j < EPC; ++j) {
+            const uint32_t q = q0 + (uint32_t)j - j0;
+            if ((uint32_t)j >= j0 && q < nq) {
+              tile[li] = f[j];
+              ++li;
+              if (++col == (uint32_t)p.IW) {
+                col = 0;
+                li += p.LW - p.IW;
+                if (++r == (uint32_t)rows_st) {  // next plane (whole-plane blocks)
+                  r = 0;
+                  li += p.PLANE - rows_st * p.LW;
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // 3. outputs: item = (plane, output row, segment of OV columns)
+  const uint32_t items_pp = (uint32_t)(rows_here * p.segs);
+  const uint32_t items = (uint32_t)nloc * items_pp;
+  for (uint32_t i = tid; i < items; i += NT) {
+    const uint32_t pp = p.multi ? fdiv(i, p.fd_items) : 0u;
+    const uint32_t rem = i - pp * items_pp;
+    const uint32_t orow = fdiv(rem, p.fd_segs);
+    const int ow0 = (int)(rem - orow * p.segs) * OV;
+    const float* src = tile + pp * p.PLANE + orow * S * p.LW + ow0 * S;
+    const float* wp = wl + pp * WST;
+    float wv[WST];
+#pragma unroll
+    for (int q = 0; q < WST / 4; ++q) {
+      const float4 t = reinterpret_cast<const float4*>(wp)[q];
+      wv[4 * q] = t.x;
+      wv[4 * q + 1] = t.y;
+      wv[4 * q + 2] = t.z;
+      wv[4 * q + 3] = t.w;
+    }
+    float acc[OV];
+#pragma unroll
+    for (int o = 0; o < OV; ++o) acc[o] = wv[KK];
+#pragma unroll
+    for (int kh = 0; kh < K; ++kh) {
+      float win[NW4 * 4];
+#pragma unroll
+      for (int q = 0; q < NW4; ++q) {
+        const float4 t = reinterpret_cast<const float4*>(src + kh * p.LW)[q];
+        win[4 * q] = t.x;
+        win[4 * q + 1] = t.y;
+        win[4 * q + 2] = t.z;
+        win[4 * q + 3] = t.w;
+      }
+#pragma unroll
+      for (int kw = 0; kw < K; ++kw)
+#pragma unroll
+        for (int o = 0; o < OV; ++o) acc[o] = fmaf(win[o * S + kw], wv[kh * K + kw], acc[o]);
+    }
+    uint32_t h[OV];
+#pragma unroll
+    for (int o = 0; o < OV; ++o) {
+      float v = acc[o];
+      if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
+      h[o] = to_bits<DT>(v);
+    }
+    const long long yo = ((long long)(plane0 + pp) * p.OH + oh0 + orow) * p.OW + ow0;
+    char* yp = static_cast<char*>(p.y) + yo * ES;
+    const uintptr_t ya = reinterpret_cast<uintptr_t>(yp);
+    if (ow0 + OV <= p.OW && (ya & 15) == 0 && (OV * ES) % 16 == 0) {
+#pragma unroll
+      for (int q = 0; q < OV * ES / 16; ++q) {
+        uint4 t;
+        if constexpr (ES == 4) t = make_uint4(h[4 * q], h[4 * q + 1], h[4 * q + 2], h[4 * q + 3]);
+        else
+          t = make_uint4(h[8 * q] | (h[8 * q + 1] << 16), h[8 * q + 2] | (h[8 * q + 3] << 16),
+                         h[8 * q + 4] | (h[8 * q + 5] << 16), h[8 * q + 6] | (h[8 * q + 7] << 16));
+        using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(u32x4{t.x, t.y, t.z, t.w}, reinterpret_cast<u32x4*>(yp) + q);
+      }
+    } else if (ow0 + OV <= p.OW && (ya & 7) == 0 && OV * ES == 8) {
+      uint2 t;
+      if constexpr (ES == 4) t = make_uint2(h[0], h[1]);
+      else t = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+      using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+      __builtin_nontemporal_store(u32x2{t.x, t.y}, reinterpret_cast<u32x2*>(yp));
+    } else {
+#pragma unroll
+      for (int o = 0; o < OV; ++o) {
+        if (ow0 + o < p.OW) {
+          if constexpr (ES == 4) reinterpret_cast<uint32_t*>(yp)[o] = h[o];
+          else reinterpret_cast<uint16_t*>(yp)[o] = (uint16_t)h[o];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ register family
+// fp16, K x K, stride S, same padding, even widths: no LDS tile at all.  One
+// wave owns a band of R output rows of pw planes; lane (plane slot, segment)
+// owns OV consecutive output columns of its plane.  The lane reads its own
+// S*OV-column chunk of every input row the band needs (all rows issued up
+// front: (R-1)*S + K loads in flight per lane), takes the halo columns on
+// either side from the neighbouring lanes' chunks (ds_bpermute; the image
+// border is zero), and accumulates each input row into the up-to-ceil(K/S)
+// output rows it feeds.  Rows above or below the image are loads at an
+// out-of-range offset, which read as zero.
+//
+// The input stays packed (two halves per dword) from load to multiply: a tap
+// pair whose first element sits at an even window position is one
+// v_dot2_f32_f16 against the packed weight pair, a tap left over is one
+// v_fma_mix_f32 on its half of the dword.  Both accumulate in fp32, and the
+// taps of a row are added in kw order (bias, then kh-outer / kw-inner).
+struct DwReg {
+  const char* x;
+  uint16_t* y;
+  const uint16_t* w;
+  const uint16_t* bias;
+  int C, IH, IW, OH, OW;
+  int segs, pw, bands, nplanes;
+  long long units;
+  unsigned long long x_bytes, y_bytes;
+  int has_clamp;
+  float cmin, cmax;
+};
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+// Cache policy of this kernel's output stores: default.  One store
+// instruction writes pw short row pieces in different planes; with the
+// non-temporal bit these partial lines bypass L2 write-combining and the
+// kernel runs at less than half the speed (measured on MI355X), whereas the
+// LDS-tiled kernel, whose lanes write one contiguous run, gains from it.
+constexpr int kStoreNT = 0;
+__device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+__device__ __forceinline__ float lo_f(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(d & 0xffffu)); }
+__device__ __forceinline__ float hi_f(uint32_t d) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(d >> 16)); }
+__device__ __forceinline__ float dot2(uint32_t x, uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, x), __builtin_bit_cast(half2_t, w), acc, false);
+}
+__device__ __forceinline__ uint32_t lane_from(uint32_t v, int src_lane) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
+}
+
+template <int K, int S, int OV, int R>
+__global__ __launch_bounds__(64) void k_dw_reg(DwReg p) {
+  constexpr int P = K / 2;
+  constexpr int CW = S * OV;           // own chunk: input columns [S*ow0, S*ow0 + CW)
+  constexpr int CD = CW / 2;           // ... as dwords
+  constexpr int HLP = (P + 1) & ~1;    // left halo columns, rounded up to whole dwords
+  constexpr int LD = HLP / 2;          // window dwords left of the own chunk
+  constexpr int MAXE = (OV - 1) * S + HLP - P + K - 1;  // last window column a tap reads
+  constexpr int WD = MAXE / 2 + 1;     // window dwords
+  constexpr int RD = WD - LD - CD;     // window dwords right of the own chunk
+  constexpr int NR = (R - 1) * S + K;  // input rows of the band
+  constexpr int NP = (K - 1) / 2;      // tap pairs per kernel row
+  static_assert(LD <= CD && RD <= CD && CD % 2 == 0, "window shape");
+  using rsrc_t = __amdgpu_buffer_rsrc_t;
+  constexpr uint32_t OOB = 0x80000000u;
+
+  // Blocks are dealt to the 8 XCDs round-robin; renumber them so each XCD
+  // runs a contiguous run of units, i.e. all bands of a plane group on one
+  // XCD at about the same time: the halo rows a band shares with its
+  // neighbours are then L2 hits instead of second HBM reads.
+  const long long G = p.units, b = blockIdx.x;
+  long long unit = b;
+  if (G >= 8) {
+    const long long xcd = b & 7, base = G >> 3, rem = G & 7;
+    unit = xcd * base + (xcd < rem ? xcd : rem) + (b >> 3);
+  }
+  const int lane = threadIdx.x;
+  const int pg = (int)(unit / p.bands), band = (int)(unit - (long long)pg * p.bands);
+  const int ps = lane / p.segs, seg = lane - ps * p.segs;
+  const int plane = pg * p.pw + ps;
+  const bool active = ps < p.pw && plane < p.nplanes;
+  const int oh0 = band * R;
+  const int col0 = seg * CW;
+  const int lim = p.IW - col0;  // valid input columns in the own chunk
+
+  // this wave's planes as buffer ranges (offsets stay far below 2^31)
+  const unsigned long long xb0 = (unsigned long long)pg * p.pw * p.IH * p.IW * 2;
+  const unsigned long long yb0 = (unsigned long long)pg * p.pw * p.OH * p.OW * 2;
+  const unsigned long long xl = p.x_bytes - xb0, yl = p.y_bytes - yb0;
+  const rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p.x) + xb0, 0,
+                                                      (int)(xl > 0x7fffffffull ? 0x7fffffffull : xl), 0x00020000);
+  const rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(p.y) + yb0, 0,
+                                                      (int)(yl > 0x7fffffffull ? 0x7fffffffull : yl), 0x00020000);
+
+  // 1. every input row of the band: one (or two) vector loads per row; the
+  //    last segment of a row that ends mid-chunk loads only its valid dwords
+  uint32_t raw[NR][CD];
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    const int ih = oh0 * S - P + j;
+    const bool rok = active && ih >= 0 && ih < p.IH;
+    const uint32_t off = (uint32_t)(((ps * p.IH + ih) * p.IW + col0) * 2);
+    if (lim >= CW) {
+#pragma unroll
+      for (int q = 0; q + 4 <= CD; q += 4) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(rok ? off + 4 * q : OOB), 0, 0);
+        raw[j][q] = v[0];
+        raw[j][q + 1] = v[1];
+        raw[j][q + 2] = v[2];
+        raw[j][q + 3] = v[3];
+      }
+      if constexpr (CD % 4 == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rx, (int)(rok ? off + 4 * (CD - 2) : OOB), 0, 0);
+        raw[j][CD - 2] = v[0];
+        raw[j][CD - 1] = v[1];
+      }
+    } else {
+#pragma unroll
+      for (int d = 0; d < CD; ++d)
+        raw[j][d] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rx, (int)(rok && 2 * d < lim ? off + 4 * d : OOB), 0, 0);
+    }
+  }
+
+  // 2. weights of this lane's plane: packed pairs (w[kw], w[kw+1]) starting at
+  //    even and at odd kw, and the two taps that can be left over, in fp32
+  uint32_t wpe[K][NP], wpo[K][NP];
+  float wfirst[K], wlast[K], bias = 0.0f;
+  {
+    const int c = active ? plane % p.C : 0;
+    uint32_t wr[K * K];
+#pragma unroll
+    for (int t = 0; t < K * K; ++t) wr[t] = p.w[c * K * K + t];
+#pragma unroll
+    for (int kh = 0; kh < K; ++kh) {
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        wpe[kh][q] = wr[kh * K + 2 * q] | (wr[kh * K + 2 * q + 1] << 16);
+        wpo[kh][q] = wr[kh * K + 2 * q + 1] | (wr[kh * K + 2 * q + 2] << 16);
+      }
+      wfirst[kh] = h2f(wr[kh * K]);
+      wlast[kh] = h2f(wr[kh * K + K - 1]);
+    }
+    if (p.bias) bias = h2f(p.bias[c]);
+  }
+  float acc[R][OV];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int o = 0; o < OV; ++o) acc[r][o] = bias;
+
+  // 3. rows in order; window dword i holds input columns col0 - HLP + 2i, +1
+  const bool has_left = seg > 0, has_right = seg + 1 < p.segs;
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    uint32_t win[WD];
+#pragma unroll
+    for (int d = 0; d < CD; ++d) win[LD + d] = raw[j][d];
+#pragma unroll
+    for (int h = 0; h < LD; ++h) {
+      const uint32_t v = lane_from(raw[j][CD - LD + h], lane - 1);
+      win[h] = has_left ? v : 0u;
+    }
+#pragma unroll
+    for (int h = 0; h < RD; ++h) {
+      const uint32_t v = lane_from(raw[j][h], lane + 1);
+      win[LD + CD + h] = has_right ? v : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int kh = j - r * S;  // compile-time after unrolling
+      if (kh >= 0 && kh < K) {
+#pragma unroll
+        for (int o = 0; o < OV; ++o) {
+          const int e0 = HLP + o * S - P;  // window column of tap kw = 0
+          float a = acc[r][o];
+          if ((e0 & 1) == 0) {
+#pragma unroll
+            for (int q = 0; q < NP; ++q) a = dot2(win[e0 / 2 + q], wpe[kh][q], a);
+            a = fmaf(lo_f(win[(e0 + K - 1) / 2]), wlast[kh], a);
+          } else {
+            a = fmaf(hi_f(win[(e0 - 1) / 2]), wfirst[kh], a);
+#pragma unroll
+            for (int q = 0; q < NP; ++q) a = dot2(win[(e0 + 1) / 2 + q], wpo[kh][q], a);
+          }
+          acc[r][o] = a;
+        }
+      }
+    }
+  }
+
+  // 4. stores: OV halves per output row, one vector store when whole
+  if (!active) return;
+  const int nvalid = min(OV, p.OW - seg * OV);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int oh = oh0 + r;
+    if (oh >= p.OH) break;
+    uint32_t h[OV];
+#pragma unroll
+    for (int o = 0; o < OV; ++o) {
+      float v = acc[r][o];
+      if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
+      h[o] = __builtin_bit_cast(uint16_t, (_Float16)v);
+    }
+    const uint32_t off = (uint32_t)(((ps * p.OH + oh) * p.OW + seg * OV) * 2);
+    if (nvalid == OV) {
+      if constexpr (OV == 8) {
+        using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+        const u32x4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, (int)off, 0, kStoreNT);
+      } else {
+        using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+        const u32x2 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        __builtin_amdgcn_raw_buffer_store_b64(v, ry, (int)off, 0, kStoreNT);
+      }
+    } else {
+#pragma unroll
+      for (int o = 0; o < OV; ++o)
+        if (o < nvalid) __builtin_amdgcn_raw_buffer_store_b16((unsigned short)h[o], ry, (int)(off + 2 * o), 0, kStoreNT);
+    }
+  }
+}
+
+// Plans the register kernel; false when d is outside its family.
+bool plan_reg(const DwDesc& d, DwReg& p, int& ov, int& R, long long& blocks) {
+  const int K = d.KH;
+  if (d.dtype != WGX_FLOAT16 || d.KW != K || (K != 3 && K != 5) || d.sH != d.sW || (d.sH != 1 && d.sH != 2) ||
+      d.pH != K / 2 || d.pW != K / 2 || d.dH != 1 || d.dW != 1)
+    return false;
+  if ((d.IW & 1) || (d.OW & 1) || (reinterpret_cast<uintptr_t>(d.x) & 3) || (reinterpret_cast<uintptr_t>(d.y) & 3) ||
+      (d.w && (reinterpret_cast<uintptr_t>(d.w) & 1)))
+    return false;
+  const int S = d.sH;
+  ov = ((d.OW + 3) / 4 * 4 < (d.OW + 7) / 8 * 8) ? 4 : 8;
+  if (S == 2 && K == 5 && ov == 8) ov = 4;  // keeps the row window in registers
+  const int segs = (d.OW + ov - 1) / ov;
+  if (segs > 64) return false;
+  const long long nplanes = (long long)d.B * d.C;
+  p.segs = segs;
+  p.pw = 64 / segs;
+  const long long groups = (nplanes + p.pw - 1) / p.pw;
+  // Band height: the fewest dead rows in the last band, ties to the taller
+  // band (fewer halo rows read twice); 4 when the grid would leave CUs idle.
+  R = 4;
+  if (groups * ((d.OH + 7) / 8) >= 2048) {
+    int best = 1 << 30;
+    for (int r : {8, 5, 4}) {
+      const int rows = (d.OH + r - 1) / r * r;  // output rows computed, dead ones included
+      if (rows < best) {
+        best = rows;
+        R = r;
+      }
+    }
+  }
+  p.bands = (d.OH + R - 1) / R;
+  p.units = groups * p.bands;
+  // a wave's planes must stay addressable with 31-bit buffer offsets
+  if ((long long)p.pw * d.IH * d.IW * 2 >= (1LL << 30) || p.units >= (1LL << 31)) return false;
+  p.x = static_cast<const char*>(d.x);
+  p.y = static_cast<uint16_t*>(d.y);
+  p.w = static_cast<const uint16_t*>(d.w);
+  p.bias = static_cast<const uint16_t*>(d.bias);
+  p.C = d.C;
+  p.IH = d.IH;
+  p.IW = d.IW;
+  p.OH = d.OH;
+  p.OW = d.OW;
+  p.nplanes = (int)nplanes;
+  p.x_bytes = (unsigned long long)nplanes * d.IH * d.IW * 2;
+  p.y_bytes = (unsigned long long)nplanes * d.OH * d.OW * 2;
+  p.has_clamp = d.has_clamp;
+  p.cmin = d.cmin;
+  p.cmax = d.cmax;
+  blocks = p.units;
+  return true;
+}
+
+template <int K, int S, int OV, int R>
+hipError_t launch_reg(const DwReg& p, long long blocks, hipStream_t s, std::string* name) {
+  if (name) {
+    char buf[64];
+    snprintf(buf, sizeof buf, "depthwise_f16_%dx%ds%d_r%dv%d", K, K, S, R, OV);
+    *name = buf;
+  }
+  if (is_dry(s)) return hipSuccess;
+  hipLaunchKernelGGL((k_dw_reg<K, S, OV, R>), dim3((unsigned)blocks), dim3(64), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int K, int S, int OV>
+hipError_t launch_reg_r(const DwReg& p, int R, long long blocks, hipStream_t s, std::string* name) {
+  if (R == 8) return launch_reg<K, S, OV, 8>(p, blocks, s, name);
+  if (R == 5) return launch_reg<K, S, OV, 5>(p, blocks, s, name);
+  return launch_reg<K, S, OV, 4>(p, blocks, s, name);
+}
+
+hipError_t launch_reg_any(const DwReg& p, int K, int S, int ov, int R, long long blocks, hipStream_t s,
+                          std::string* name) {
+  if (K == 3 && S == 1) return ov == 8 ? launch_reg_r<3, 1, 8>(p, R, blocks, s, name) : launch_reg_r<3, 1, 4>(p, R, blocks, s, name);
+  if (K == 3 && S == 2) return ov == 8 ? launch_reg_r<3, 2, 8>(p, R, blocks, s, name) : launch_reg_r<3, 2, 4>(p, R, blocks, s, name);
+  if (K == 5 && S == 1) return ov == 8 ? launch_reg_r<5, 1, 8>(p, R, blocks, s, name) : launch_reg_r<5, 1, 4>(p, R, blocks, s, name);
+  return launch_reg_r<5, 2, 4>(p, R, blocks, s, name);
+}
+
+constexpr int kFastLds = 40 * 1024;  // LDS budget of one block (4 blocks per CU)
+
 template <int DT>
 hipError_t launch_dt(const DwParams& p, int blocks, size_t lds, hipStream_t s, std::string* name) {
   char buf[64];
@@ -151,9 +741,125 @@ hipError_t launch_dt(const DwParams& p, int blocks, size_t lds, hipStream_t s, s
   return go(k_depthwise<DT, 0, 0>, "kxk");
 }
 
+template <int DT, int K, int S, int OV>
+hipError_t launch_fast(const DwFast& p, int blocks, size_t lds, hipStream_t s, std::string* name) {
+  if (name) {
+    char buf[64];
+    snprintf(buf, sizeof buf, "depthwise_%s_%dx%ds%d_v%d", DT == WGX_FLOAT32 ? "f32" : DT == WGX_FLOAT16 ? "f16" : "bf16",
+             K, K, S, OV);
+    *name = buf;
+  }
+  if (is_dry(s)) return hipSuccess;
+  hipLaunchKernelGGL((k_dw_fast<DT, K, S, OV>), dim3(blocks), dim3(NT), lds, s, p);
+  return hipGetLastError();
+}
+
+template <int DT, int K, int S>
+hipError_t launch_fast_ov(const DwFast& p, int ov, int blocks, size_t lds, hipStream_t s, std::string* name) {
+  return ov == 8 ? launch_fast<DT, K, S, 8>(p, blocks, lds, s, name) : launch_fast<DT, K, S, 4>(p, blocks, lds, s, name);
+}
+
+template <int DT>
+hipError_t launch_fast_dt(const DwFast& p, int K, int S, int ov, int blocks, size_t lds, hipStream_t s,
+                          std::string* name) {
+  if (K == 3) return S == 1 ? launch_fast_ov<DT, 3, 1>(p, ov, blocks, lds, s, name)
+                            : launch_fast_ov<DT, 3, 2>(p, ov, blocks, lds, s, name);
+  return S == 1 ? launch_fast_ov<DT, 5, 1>(p, ov, blocks, lds, s, name)
+                : launch_fast_ov<DT, 5, 2>(p, ov, blocks, lds, s, name);
+}
+
+// Plans the fast kernel for d; false when the shape is outside its family or
+// its LDS tile does not fit.
+bool plan_fast(const DwDesc& d, DwFast& p, int& ov, int& blocks, size_t& lds) {
+  const int K = d.KH;
+  if (d.KW != K || (K != 3 && K != 5) || d.sH != d.sW || (d.sH != 1 && d.sH != 2) || d.pH != K / 2 ||
+      d.pW != K / 2 || d.dH != 1 || d.dW != 1)
+    return false;
+  const int S = d.sH, P = K / 2;
+  const int es = d.dtype == WGX_FLOAT32 ? 4 : 2;
+  // output segment per lane: 8, or 4 where that wastes fewer lanes on the row end
+  ov = ((d.OW + 3) / 4 * 4 < (d.OW + 7) / 8 * 8) ? 4 : 8;
+  const int segs = (d.OW + ov - 1) / ov;
+  const int nw4 = ((ov - 1) * S + K + 3) / 4;
+  const int wst = (K * K + 1 + 3) / 4 * 4;
+  int LW = (segs - 1) * ov * S + 4 * nw4;
+  if (LW < P + d.IW) LW = P + d.IW;
+  LW = (LW + 3) / 4 * 4;
+  const long long nplanes = (long long)d.B * d.C;
+  const long long lr_full = std::max((long long)(d.OH - 1) * S + K, (long long)d.IH + P);
+  const long long plane_bytes = lr_full * LW * 4 + wst * 4;
+  p.multi = plane_bytes <= kFastLds;
+  if (p.multi) {
+    int ppb = (768 + d.OH * segs - 1) / (d.OH * segs);
+    ppb = std::min<long long>(ppb, kFastLds / plane_bytes);
+    ppb = std::min<long long>(ppb, std::max<long long>(1, nplanes / 512));  // >= 2 blocks per CU
+    p.ppb = std::max(ppb, 1);
+    p.toh = d.OH;
+    p.bands = 1;
+    p.LR = (int)lr_full;
+    blocks = (int)((nplanes + p.ppb - 1) / p.ppb);
+  } else {
+    p.ppb = 1;
+    const int rows_fit = (kFastLds / 4 - wst) / LW;  // LDS rows of one band
+    const int toh_lds = (rows_fit - K) / S + 1;
+    if (rows_fit < K || toh_lds < 1) return false;
+    int toh = std::min(d.OH, std::max(1, (1024 + segs - 1) / segs));
+    toh = std::min(toh, toh_lds);
+    p.toh = toh;
+    p.bands = (d.OH + toh - 1) / toh;
+    p.LR = (toh - 1) * S + K;
+    if (nplanes * p.bands > INT32_MAX) return false;
+    blocks = (int)(nplanes * p.bands);
+  }
+  p.PLANE = p.LR * LW;
+  p.LW = LW;
+  p.segs = segs;
+  p.nplanes = (int)nplanes;
+  lds = ((size_t)p.ppb * p.PLANE + (size_t)p.ppb * wst) * 4;
+  if (lds > 64 * 1024) return false;
+  const uintptr_t xv = reinterpret_cast<uintptr_t>(d.x);
+  p.xa = reinterpret_cast<const char*>(xv & ~uintptr_t(15));
+  p.lead0 = (uint32_t)((xv & 15) / es);
+  p.x_end = (xv & 15) + (unsigned long long)nplanes * d.IH * d.IW * es;
+  p.w = d.w;
+  p.bias = d.bias;
+  p.y = d.y;
+  p.C = d.C;
+  p.IH = d.IH;
+  p.IW = d.IW;
+  p.OH = d.OH;
+  p.OW = d.OW;
+  p.fd_plane = make_fastdiv((uint32_t)(d.IH * d.IW));
+  p.fd_iw = make_fastdiv((uint32_t)d.IW);
+  p.fd_items = make_fastdiv((uint32_t)(d.OH * segs));
+  p.fd_segs = make_fastdiv((uint32_t)segs);
+  p.has_clamp = d.has_clamp;
+  p.cmin = d.cmin;
+  p.cmax = d.cmax;
+  return (long long)p.ppb * d.IH * d.IW < (1LL << 30);
+}
+
 }  // namespace
 
 hipError_t launch_depthwise(const DwDesc& d, hipStream_t s, std::string* name) {
+  {
+    DwFast f;
+    int ov = 8, blocks = 0;
+    size_t lds = 0;
+    // WGX_DW_KERNEL=lds|generic narrows the choice (A/B timing of the variants)
+    static const char* only = getenv("WGX_DW_KERNEL");
+    const bool allow_reg = !only, allow_lds = !only || only[0] == 'l';
+    DwReg rp;
+    int rov = 8, R = 4;
+    long long rblocks = 0;
+    if (allow_reg && plan_reg(d, rp, rov, R, rblocks)) return launch_reg_any(rp, d.KH, d.sH, rov, R, rblocks, s, name);
+    if (allow_lds && plan_fast(d, f, ov, blocks, lds)) {
+      const int K = d.KH, S = d.sH;
+      if (d.dtype == WGX_FLOAT16) return launch_fast_dt<WGX_FLOAT16>(f, K, S, ov, blocks, lds, s, name);
+      if (d.dtype == WGX_BFLOAT16) return launch_fast_dt<WGX_BFLOAT16>(f, K, S, ov, blocks, lds, s, name);
+      return launch_fast_dt<WGX_FLOAT32>(f, K, S, ov, blocks, lds, s, name);
+    }
+  }
   DwParams p;
   p.x = d.x;
   p.w = d.w;

@@ -197,7 +197,11 @@ struct wgx_ctx {
     void* p = nullptr;
     if (d->has_dev) {
       if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-      if (hipMemset(p, 0, bytes) != hipSuccess) {
+      // Zero-fill on the context's own stream and wait for it: the stream is
+      // non-blocking, so a fill on the null stream would not be ordered with
+      // the uploads and launches that follow on it (a late fill could land on
+      // top of uploaded data).
+      if (hipMemsetAsync(p, 0, bytes, d->stream) != hipSuccess || hipStreamSynchronize(d->stream) != hipSuccess) {
         hipFree(p);
         return nullptr;
       }
