@@ -139,3 +139,39 @@ def test_bmm_trans_and_ragged(gpu_ctx, orc, pkg):
             gpu_ctx.sync()
             ref, refa = orc.gemm_f64(A, B)
             assert_parity(to.get_f32(), ref, refa, dtype, 70, f"bmm {dtype} tb={tb}")
+
+
+@pytest.mark.parametrize("tile", ["256x192b", "192x256b"])
+def test_large_tile_kernel_edges(gpu_ctx, orc, pkg, tile, monkeypatch):
+    """The large-tile [N, K] kernel forced onto ragged shapes: partial tiles
+    in M and N, K with a partial last slice (K % 32 != 0), several tiles per
+    block, a batch of transposed-B products, alpha/beta and both dtypes."""
+    I = pkg.inputs
+    monkeypatch.setenv("WGX_MFMA_TILE", tile)
+    for i, (M, N, K) in enumerate([(300, 200, 104), (513, 385, 136), (256, 192, 32), (1024, 768, 2056),
+                                   (40, 24, 64)]):
+        for dtype in ("float16", "bfloat16"):
+            A = round_in(I.uniform(1400 + i, (M, K), -1, 1), dtype)
+            B = round_in(I.uniform(1500 + i, (K, N), -1, 1), dtype)
+            bias = round_in(I.uniform(1600 + i, (N,), -0.5, 0.5), dtype)
+            alpha, beta = (0.5, 2.0) if i % 2 else (1.0, 1.0)
+            got, kernel = run_mm(gpu_ctx, A, np.ascontiguousarray(B.T), dtype, bias=bias, trans_b=True,
+                                 alpha=alpha, beta=beta)
+            assert kernel.endswith("_nk_big") and tile[:-1] in kernel, kernel
+            ref, refa = orc.gemm_f64(A, B)
+            ref = alpha * ref + beta * bias
+            refa = abs(alpha) * refa + abs(beta) * np.abs(bias)
+            assert_parity(got, ref, refa, dtype, K, f"big {tile} {dtype} {M}x{N}x{K} {kernel}")
+    A = round_in(I.uniform(1700, (3, 260, 72), -1, 1), "float16")
+    B = round_in(I.uniform(1701, (3, 72, 200), -1, 1), "float16")
+    ta = gpu_ctx.from_numpy(A, "float16")
+    tbb = gpu_ctx.from_numpy(np.ascontiguousarray(B.transpose(0, 2, 1)), "float16")
+    to = gpu_ctx.tensor("float16", [3, 260, 200])
+    gpu_ctx.reset()
+    gpu_ctx.bmm(ta, tbb, to, trans_b=True)
+    kernel = gpu_ctx.last_kernel
+    gpu_ctx.submit()
+    gpu_ctx.sync()
+    assert kernel.endswith("_nk_big"), kernel
+    ref, refa = orc.gemm_f64(A, B)
+    assert_parity(to.get_f32(), ref, refa, "float16", 72, f"big bmm {tile} {kernel}")

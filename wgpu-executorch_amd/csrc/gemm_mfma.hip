@@ -69,6 +69,7 @@ struct KParams {
   int batch;
   int splits, kchunk;  // split-K: K ranges per tile, K slices per range
   float* ws;           // split-K partial sums, [splits][batch][M][N]
+  int nt_store;        // large-tile kernel: non-temporal output stores
 };
 
 template <bool BF>
@@ -577,6 +578,13 @@ __device__ __forceinline__ void dma16(rsrc_t r, const uint16_t* lds_wave_base, u
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :: "s"(la), "v"(voff), "s"(r) : "memory", "m0");
 }
+// The same with the slice's k offset in the instruction's scalar offset, so a
+// lane's vector offset stays fixed for a whole tile (no per-slice VALU work).
+__device__ __forceinline__ void dma16s(rsrc_t r, const void* lds_wave_base, uint32_t voff, uint32_t soff) {
+  const uint32_t la = (uint32_t)(uintptr_t)lds_wave_base;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(la), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
 __device__ __forceinline__ void st_b64(uint2 v, rsrc_t r, uint32_t off) {
   using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
   const u32x2 d = {v.x, v.y};
@@ -701,6 +709,9 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     int tile, sp, kbase, kts;  // output tile, K range, its first k and slice count
     unsigned long long cmask;
     uint32_t bias_h;
+    // byte offset of this lane's 16-byte DMA chunk at k = 0 (OOB for rows past
+    // the operand's edge); a slice adds k0 * ES as the scalar offset
+    uint32_t va[CHA], vb[CHB > 0 ? CHB : 1];
   };
   const int nl = tid % BN;
   const int krun = tid / BN;
@@ -738,6 +749,21 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
       const uint32_t off = (tid < cnt && b0 + tid < lim) ? (uint32_t)(b0 + tid) * ES : OOB;
       s.bias_h = ES == 4 ? ld_b32(rbias, off) : ld_b16(rbias, off);
     }
+#pragma unroll
+    for (int i = 0; i < CHA; ++i) {
+      const int row = (i * NW + wave) * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+      s.va[i] = row < mrows ? (uint32_t)(((long long)row * p.lda + chunk * EPC) * ES) : OOB;
+    }
+    if constexpr (BDMA) {
+      const int nrows = min(BN, N - s.n0);
+#pragma unroll
+      for (int i = 0; i < CHB; ++i) {
+        const int row = (i * NW + wave) * 8 + (lane >> 3);
+        const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+        s.vb[i] = row < nrows ? (uint32_t)(((long long)row * p.ldb + chunk * EPC) * ES) : OOB;
+      }
+    }
     s.gn_col = s.n0 + nl;
     s.colbase = 0;
     s.cmask = 0ull;
@@ -773,6 +799,23 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
       const uint32_t off = (uint32_t)(row * ld + k0 + chunk * EPC) * ES;
       dma16(rs, reinterpret_cast<const uint16_t*>(dst + (i * NW + wave) * 1024),
             k0 + chunk * EPC < K ? off : OOB);
+    }
+  };
+  // One slice (k0 = first k) of A, and of B in the B_NK form, into stage dst.
+  // A slice that reaches past K takes the masked form above (every chunk
+  // past K reads zero); a whole slice uses the tile's fixed lane offsets.
+  auto dma_slice = [&](const TileState& st, int k0, char* da, char* db) {
+    if (k0 + BK <= K) {
+      const uint32_t so = (uint32_t)k0 * ES;
+#pragma unroll
+      for (int i = 0; i < CHA; ++i) dma16s(st.ra, da + (i * NW + wave) * 1024, st.va[i], so);
+      if constexpr (BDMA) {
+#pragma unroll
+        for (int i = 0; i < CHB; ++i) dma16s(st.rb, db + (i * NW + wave) * 1024, st.vb[i], so);
+      }
+    } else {
+      dma_rows(st.ra, p.lda, k0, da, std::integral_constant<int, CHA>{});
+      if constexpr (BDMA) dma_rows(st.rb, p.ldb, k0, db, std::integral_constant<int, CHB>{});
     }
   };
   struct BRegs {
@@ -892,14 +935,19 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
       for (int j = 0; j < TN; ++j)
         b[j] = *reinterpret_cast<const uint4*>(sb + swz(wn * WN + j * 32 + frow, kk * 2 + fc));
     };
+    // Fragments of step kk+1 are issued before the MFMAs of step kk and the
+    // order is pinned (sched_barrier): left alone, the scheduler sinks each
+    // LDS read to just before its MFMA and exposes the LDS latency every step.
     frags(0, af[0], bfr[0]);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {  // 4 steps of 2 chunks = one 128-byte row
       if (kk + 1 < 4) frags(kk + 1, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma_frag<DT>(bfr[kk & 1][j], af[kk & 1][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -910,20 +958,27 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
 
   // the first NS-1 slices of a tile: DMA into stages 0..NS-2; register-staged
   // B slice 0 goes to LDS at the top of the tile loop, slice 1 in step 0
+  // Slices past the unit's K range are not loaded at all (so no load can
+  // reach past the operand); the waits below count only issued slices.
   auto prologue = [&](const TileState& st) {
     const int k0 = st.kbase;
     if constexpr (!BDMA) load_b(st, k0, RB);
-    dma_rows(st.ra, p.lda, k0, stA(std::integral_constant<int, 0>{}), std::integral_constant<int, CHA>{});
-    if constexpr (BDMA)
-      dma_rows(st.rb, p.ldb, k0, stB(std::integral_constant<int, 0>{}), std::integral_constant<int, CHB>{});
-    dma_rows(st.ra, p.lda, k0 + BK, stA(std::integral_constant<int, 1>{}), std::integral_constant<int, CHA>{});
-    if constexpr (BDMA)
-      dma_rows(st.rb, p.ldb, k0 + BK, stB(std::integral_constant<int, 1>{}), std::integral_constant<int, CHB>{});
+    dma_slice(st, k0, stA(std::integral_constant<int, 0>{}), stB(std::integral_constant<int, 0>{}));
+    if (st.kts > 1)
+      dma_slice(st, k0 + BK, stA(std::integral_constant<int, 1>{}), stB(std::integral_constant<int, 1>{}));
     if constexpr (NS > 3) {
-      dma_rows(st.ra, p.lda, k0 + 2 * BK, stA(std::integral_constant<int, 2>{}), std::integral_constant<int, CHA>{});
-      if constexpr (BDMA)
-        dma_rows(st.rb, p.ldb, k0 + 2 * BK, stB(std::integral_constant<int, 2>{}), std::integral_constant<int, CHB>{});
+      if (st.kts > 2)
+        dma_slice(st, k0 + 2 * BK, stA(std::integral_constant<int, 2>{}), stB(std::integral_constant<int, 2>{}));
     }
+  };
+  // s_waitcnt until slice `need` has landed, given that the unit's slices up
+  // to min(newest, kts - 1) were issued after it (n of them, 0 <= n <= NS-2)
+  auto wait_slice = [&](int need, int newest, int kts) {
+    const int last = min(newest, kts - 1);
+    const int n = last > need ? last - need : 0;
+    if (n >= 2 && NS > 3) wait_vm<(NS > 3 ? 2 : 0) * DMAS>();
+    else if (n >= 1) wait_vm<DMAS>();
+    else wait_vm<0>();
   };
 
   // Step t (stage s = t % NS): request slice t+NS-1 into the stage read last
@@ -934,15 +989,13 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     constexpr int S1 = (S + 1) % NS, SL = (S + NS - 1) % NS;
     using I1 = std::integral_constant<int, S1>;
     using IL = std::integral_constant<int, SL>;
-    // slices past this unit's K range (the next range's, or past K: zeros)
-    // are loaded but never multiplied
+    // register-staged B of slice t+1 (past K it reads zeros, never multiplied)
     if constexpr (!BDMA) load_b(cur, cur.kbase + (t + 1) * BK, RB);
-    dma_rows(cur.ra, p.lda, cur.kbase + (t + NS - 1) * BK, stA(IL{}), std::integral_constant<int, CHA>{});
-    if constexpr (BDMA)
-      dma_rows(cur.rb, p.ldb, cur.kbase + (t + NS - 1) * BK, stB(IL{}), std::integral_constant<int, CHB>{});
+    if (t + NS - 1 < cur.kts)
+      dma_slice(cur, cur.kbase + (t + NS - 1) * BK, stA(IL{}), stB(IL{}));
     compute(stA(s_tag), stB(s_tag));
     if constexpr (!BDMA) store_b(stB(I1{}), RB);
-    wait_vm<(NS - 2) * DMAS>();  // slice t+1 landed, the later ones may still run
+    wait_slice(t + 1, t + NS - 1, cur.kts);  // slice t+1 landed, later ones may still run
     __syncthreads();
   };
 
@@ -957,7 +1010,7 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    wait_vm<(NS - 2) * DMAS>();  // slice 0 landed (slices 1.. may still run)
+    wait_slice(0, NS - 2, cur.kts);  // slice 0 landed (slices 1.. may still run)
     __syncthreads();
 
     const int kts = cur.kts;
@@ -1058,6 +1111,281 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
     if (next >= nunits) break;
     unit = next;
   }
+}
+
+// ============================================================ large-tile kernel
+// C = epilogue(A * B^T) with A [M, K] and B [N, K], both k-contiguous (the
+// nn.Linear / W^T form of addmm, and bmm with a transposed right operand),
+// float16 or bfloat16, for shapes with enough tiles of 256 rows.
+//
+// Why a second kernel: measured on MI355X, the L2 -> LDS path moves 35-50
+// bytes per clock per CU (with 64-128 KB in flight), 128-bit LDS reads about
+// 64 B/clk per CU.  A 128 x 128 block tile at the full MFMA rate needs
+// 64 B/clk of operand traffic; a 256 x 192 tile needs 37 B/clk, and its
+// 128 x 96 wave tiles need the fewest LDS fragment bytes per MFMA that fit in
+// registers.  So: 256-row tiles, 4 waves (one per SIMD, 12 accumulators),
+// RB-byte LDS rows (RB = 64: a K slice of 32, chunk c of row r stored at
+// c ^ ((r / 4) % 4); RB = 128: a slice of 64, chunk c at c ^ ((r / 2) % 8);
+// either way the 16 rows one 128-bit read touches per cycle cover all 64
+// banks), NS stages, all loads LDS-DMA with the slice's k offset in the
+// scalar offset, one barrier per slice.  The epilogue goes through the (then
+// idle) stage memory so that every store instruction writes whole rows of the
+// tile: full 128-byte lines, which the memory system absorbs at close to copy
+// speed.  The fragment reads (about 74 B/clk at the full MFMA rate) plus the
+// DMA writes bound this loop by LDS bandwidth at roughly 55-60% of the MFMA
+// peak.
+__device__ __forceinline__ int swz64(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+int device_cus();
+
+template <int BM, int BN, int WGM, int WGN, bool BF, int NS, int RB>
+__global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_nk(KParams p) {
+  constexpr int NW = WGM * WGN, NT = NW * 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  constexpr int ES = 2, EPC = 8, BK = RB / ES;  // RB: LDS row bytes (64 or 128)
+  constexpr int CPR = RB / 16, RPI = 1024 / RB;  // chunks per row, rows per DMA instruction
+  constexpr int KS = RB / 32;                    // k-steps of 16 per slice
+  constexpr int STAGE = (BM + BN) * RB;                 // bytes per stage
+  constexpr int CHA = BM * RB / 1024 / NW;              // DMA instructions per wave per slice: A
+  constexpr int CHB = BN * RB / 1024 / NW;              // ... B
+  constexpr int DMAS = CHA + CHB;
+  constexpr int CP = BN * ES + 16;                      // epilogue LDS row pitch
+  constexpr int EROWS = BM * CP <= NS * STAGE ? BM : BM / 2;  // rows per epilogue pass
+  constexpr int BMAX = BM > BN ? BM : BN;
+  static_assert(TM >= 1 && TN >= 1 && CHA >= 1 && CHB >= 1, "tile shape");
+  static_assert(BM * RB % (1024 * NW) == 0 && BN * RB % (1024 * NW) == 0, "DMA split");
+  static_assert(EROWS * CP <= NS * STAGE && EROWS % WM == 0, "epilogue staging");
+  static_assert((NS - 1) * DMAS < 64 && NS >= 2 && NS <= 5 && (RB == 64 || RB == 128), "stages");
+
+  // 16-byte chunk c of LDS row r is stored at chunk swzc(r, c): with 64-byte
+  // rows c ^ ((r/4)%4), with 128-byte rows c ^ ((r/2)%8); the 16 rows one
+  // 128-bit fragment read touches per cycle then cover all 64 banks
+  auto swzc = [](int r, int c) { return RB == 64 ? c ^ ((r >> 2) & 3) : c ^ ((r >> 1) & 7); };
+  auto swzr = [&](int r, int c) { return r * RB + (swzc(r, c) << 4); };
+  __shared__ __attribute__((aligned(1024))) char stg[NS * STAGE];
+  __shared__ __attribute__((aligned(16))) float sbias[BMAX];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int M = p.M, N = p.N, K = p.K;
+  const int KT = (K + BK - 1) / BK;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_mn = tiles_m * p.tiles_n;
+  const int ntiles = tiles_mn * p.batch;
+  const int G = gridDim.x;
+  const int rbk = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const char* Ab = reinterpret_cast<const char*>(p.A);
+  const char* Bb = reinterpret_cast<const char*>(p.B);
+  char* Cb = reinterpret_cast<char*>(p.C);
+  const bool cvec = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0) && ((p.sC & 7) == 0);
+
+  for (int tile = rbk; tile < ntiles; tile += G) {
+    // grouped tile order: p.gm m-tiles are walked first, then n (a run of
+    // consecutive tiles -- one XCD's share -- covers a compact rectangle)
+    const int z = tile / tiles_mn, r = tile % tiles_mn;
+    const int gsz = p.gm * p.tiles_n;
+    const int grp = r / gsz, rr = r - grp * gsz;
+    const int gmh = min(p.gm, tiles_m - grp * p.gm);
+    const int m0 = (grp * p.gm + rr % gmh) * BM;
+    const int n0 = (rr / gmh) * BN;
+    const int mrows = min(BM, M - m0), nrows = min(BN, N - n0);
+    const rsrc_t ra = make_rsrc(Ab + ((long long)z * p.sA + (long long)m0 * p.lda) * ES,
+                                (uint32_t)((mrows - 1) * p.lda + K) * ES);
+    const rsrc_t rbf = make_rsrc(Bb + ((long long)z * p.sB + (long long)n0 * p.ldb) * ES,
+                                 (uint32_t)((nrows - 1) * p.ldb + K) * ES);
+    // this lane's DMA chunk of each instruction: LDS row (i*NW + wave)*RPI +
+    // lane/CPR, stored chunk lane%CPR, which holds logical chunk swzc(row, lane%CPR)
+    uint32_t va[CHA], vb[CHB];
+#pragma unroll
+    for (int i = 0; i < CHA; ++i) {
+      const int row = (i * NW + wave) * RPI + lane / CPR, chunk = swzc(row, lane % CPR);
+      va[i] = row < mrows ? (uint32_t)(((long long)row * p.lda + chunk * EPC) * ES) : OOB;
+    }
+#pragma unroll
+    for (int i = 0; i < CHB; ++i) {
+      const int row = (i * NW + wave) * RPI + lane / CPR, chunk = swzc(row, lane % CPR);
+      vb[i] = row < nrows ? (uint32_t)(((long long)row * p.ldb + chunk * EPC) * ES) : OOB;
+    }
+    // slice s into stage s % NS; a slice reaching past K masks its chunks
+    auto issue = [&](int sl) {
+      char* base = stg + (sl % NS) * STAGE;
+      const int k0 = sl * BK;
+      if (k0 + BK <= K) {
+        const uint32_t so = (uint32_t)k0 * ES;
+#pragma unroll
+        for (int i = 0; i < CHA; ++i) dma16s(ra, base + (i * NW + wave) * 1024, va[i], so);
+#pragma unroll
+        for (int i = 0; i < CHB; ++i) dma16s(rbf, base + BM * RB + (i * NW + wave) * 1024, vb[i], so);
+      } else {
+#pragma unroll
+        for (int i = 0; i < CHA; ++i) {
+          const int row = (i * NW + wave) * RPI + lane / CPR, chunk = swzc(row, lane % CPR);
+          const bool ok = row < mrows && k0 + chunk * EPC < K;
+          dma16(ra, reinterpret_cast<const uint16_t*>(base + (i * NW + wave) * 1024),
+                ok ? (uint32_t)((row * p.lda + k0 + chunk * EPC) * ES) : OOB);
+        }
+#pragma unroll
+        for (int i = 0; i < CHB; ++i) {
+          const int row = (i * NW + wave) * RPI + lane / CPR, chunk = swzc(row, lane % CPR);
+          const bool ok = row < nrows && k0 + chunk * EPC < K;
+          dma16(rbf, reinterpret_cast<const uint16_t*>(base + BM * RB + (i * NW + wave) * 1024),
+                ok ? (uint32_t)((row * p.ldb + k0 + chunk * EPC) * ES) : OOB);
+        }
+      }
+    };
+
+    // bias of the tile, scaled by beta, parked in LDS (the previous tile's
+    // epilogue ended with a barrier, so nobody reads the old values)
+    if (p.bias_mode != BIAS_NONE) {
+      const bool col = p.bias_mode == BIAS_COL;
+      const int lim = col ? N : M, b0 = col ? n0 : m0, cnt = col ? BN : BM;
+      const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)lim * ES);
+      for (int i = tid; i < cnt; i += NT) {
+        const uint32_t off = b0 + i < lim ? (uint32_t)(b0 + i) * ES : OOB;
+        sbias[i] = p.beta * to_f32<BF ? DT_BF16 : DT_F16>(ld_b16(rbias, off));
+      }
+    }
+
+#pragma unroll 1
+    for (int sl = 0; sl < NS - 1; ++sl)
+      if (sl < KT) issue(sl);
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int frow = lane & 31, fc = lane >> 5;
+    auto frags = [&](int sl, int kk, uint4* a, uint4* b) {
+      const char* sa = stg + (sl % NS) * STAGE;
+      const char* sb = sa + BM * RB;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const uint4*>(sa + swzr(wm * WM + i * 32 + frow, kk * 2 + fc));
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = *reinterpret_cast<const uint4*>(sb + swzr(wn * WN + j * 32 + frow, kk * 2 + fc));
+    };
+    // slice `need` has landed once at most the slices issued after it, up
+    // to slice `newest` (clipped to the last one), are still outstanding
+    auto wait_for = [&](int need, int newest) {
+      const int after = min(newest, KT - 1) - need;
+      if (after >= 3) wait_vm<3 * DMAS>();
+      else if (after == 2) wait_vm<2 * DMAS>();
+      else if (after == 1) wait_vm<DMAS>();
+      else wait_vm<0>();
+    };
+    // Software pipeline over (slice, k-step): the fragments of the next
+    // k-step are read while the current one's MFMAs run, also across slices.
+    // The barrier of slice t+1 sits before the last k-step of slice t, so the
+    // MFMAs issued before it keep the matrix cores busy while the waves meet;
+    // past it slice t+1 is visible to every wave, and every wave holds all of
+    // slice t in registers, so slice t's stage is refilled with slice t+NS.
+    uint4 fa[2][TM], fb[2][TN];
+    wait_for(0, NS - 2);
+    __syncthreads();
+    if (NS - 1 < KT) issue(NS - 1);
+    frags(0, 0, fa[0], fb[0]);
+    for (int t = 0; t < KT; ++t) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int cur = kk & 1, nxt = cur ^ 1;  // KS is even: a slice starts in buffer 0
+        if (kk + 1 < KS) {
+          frags(t, kk + 1, fa[nxt], fb[nxt]);
+        } else if (t + 1 < KT) {
+          wait_for(t + 1, t + NS - 1);
+          __syncthreads();
+          if (t + NS < KT) issue(t + NS);
+          frags(t + 1, 0, fa[nxt], fb[nxt]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma<BF>(fb[cur][j], fa[cur][i], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __syncthreads();  // every wave is done with the stages: they hold the C tile now
+
+    // ------------------------------------------------------------ epilogue
+    // acc[i][j] holds C^T: this lane owns row wm*WM + i*32 + lane%32 and, per
+    // register group g, columns wn*WN + j*32 + 8g + 4*(lane/32) + 0..3.
+#pragma unroll
+    for (int q = 0; q < BM / EROWS; ++q) {
+      if ((wm * WM) / EROWS == q) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int row = wm * WM + i * 32 + frow;
+          const float rowb = p.bias_mode == BIAS_ROW ? sbias[row] : 0.0f;
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int col = wn * WN + j * 32 + 8 * g + 4 * fc;
+              float4 bc = make_float4(0.f, 0.f, 0.f, 0.f);
+              if (p.bias_mode == BIAS_COL) bc = *reinterpret_cast<const float4*>(&sbias[col]);
+              const float bb[4] = {bc.x, bc.y, bc.z, bc.w};
+              uint32_t h[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
+                if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+                h[e] = st_bits<BF>(x);
+              }
+              *reinterpret_cast<uint2*>(stg + (row - q * EROWS) * CP + col * ES) =
+                  make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+            }
+          // keep the accumulator reads of one row block together (the
+          // scheduler would otherwise hoist them all and run out of VGPRs)
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      __syncthreads();
+      // EROWS rows of BN columns: 16 bytes per lane, lanes along the rows
+      constexpr int PPR = BN * ES / 16;  // 16-byte pieces per row
+      for (int idx = tid; idx < EROWS * PPR; idx += NT) {
+        const int rr2 = idx / PPR, pc = idx - rr2 * PPR;
+        const int grow = m0 + q * EROWS + rr2, gcol = n0 + pc * EPC;
+        if (grow >= M || gcol >= N) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(stg + rr2 * CP + pc * 16);
+        uint16_t* dst = reinterpret_cast<uint16_t*>(Cb) + (long long)z * p.sC + (long long)grow * p.ldc + gcol;
+        if (cvec && gcol + EPC <= N) {
+          using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+          const u32x4 w4 = {v.x, v.y, v.z, v.w};
+          if (p.nt_store) __builtin_nontemporal_store(w4, reinterpret_cast<u32x4*>(dst));
+          else *reinterpret_cast<u32x4*>(dst) = w4;
+        } else {
+          const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int e = 0; e < EPC; ++e)
+            if (gcol + e < N) dst[e] = (uint16_t)(u[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, bool BF, int NS, int RB>
+hipError_t launch_nk(const KParams& kp, int batch, hipStream_t s) {
+  auto fn = k_gemm_nk<BM, BN, WGM, WGN, BF, NS, RB>;
+  if (is_dry(s)) return hipSuccess;
+  const long long ntiles = (long long)((kp.M + BM - 1) / BM) * kp.tiles_n * batch;
+  long long grid = device_cus();  // one block per CU (the stages take most of the LDS)
+  if (grid > ntiles) grid = ntiles;
+  KParams k2 = kp;
+  k2.batch = batch;
+  {
+    const int tiles_m = (kp.M + BM - 1) / BM;
+    const double per_xcd = (double)(grid < 8 ? 1 : grid / 8);
+    int gm = (int)lround(sqrt(per_xcd * BN / BM));
+    k2.gm = gm < 1 ? 1 : (gm > tiles_m ? tiles_m : gm);
+  }
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WGM * WGN * 64), 0, s, k2);
+  return hipGetLastError();
 }
 
 // Split-K reduction: C = epilogue(sum over ranges of ws[r]), the ranges
@@ -1284,7 +1612,20 @@ struct Plan {
   int es;
   Tile t;
   bool pipelined;  // runs k_gemm3 (split-K capable)
+  bool big;        // runs k_gemm_nk with tile bt
+  Tile bt;
 };
+
+// Large-tile kernel shapes (one block of 4 waves per CU).
+constexpr Tile kBigTiles[] = {{256, 192, 2, 2}, {192, 256, 2, 2}, {256, 128, 2, 2}};
+
+// The cost model of choose_tile for one tile: rounds over the CUs times the
+// tile area per round, weighted by the tile's operand-reuse penalty.
+double tile_cost(const Tile& t, int M, int N, int batch, int per_cu) {
+  const long long tiles = (long long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
+  const double rounds = ceil((double)tiles / (256.0 * per_cu));
+  return rounds * t.bm * t.bn * per_cu * (1.0 + 64.0 / t.bm + 64.0 / t.bn);
+}
 
 Plan make_plan(const GemmDesc& d) {
   Plan pl;
@@ -1308,6 +1649,27 @@ Plan make_plan(const GemmDesc& d) {
     pl.pipelined = pl.avec && pl.bvec == (d.bmode != B_CONV) && !use_v2() &&
                    !(pl.t.bm == 256 && pl.t.bn == 256);
   if (pl.bf && d.bmode == B_CONV) pl.pipelined = false;
+  // the large-tile kernel for the [N, K] form when its tiles cost less
+  pl.big = false;
+  if (!pl.f32 && d.bmode == B_NK && pl.avec && pl.bvec && !use_v2()) {
+    const int per_cu = pl.t.wgm * pl.t.wgn == 8 || tile_lds(pl.t, d.bmode, d.K) > 80 * 1024 ? 1 : 2;
+    double best = tile_cost(pl.t, d.M, d.N, d.batch, per_cu);
+    const char* force = getenv("WGX_MFMA_TILE");
+    for (const Tile& t : kBigTiles) {
+      const double c = tile_cost(t, d.M, d.N, d.batch, 1);
+      bool take = c < best;
+      if (force) {  // "BMxBNb" picks a large tile by name, any other value keeps k_gemm3's
+        int bm = 0, bn = 0;
+        char tag = 0;
+        take = sscanf(force, "%dx%d%c", &bm, &bn, &tag) == 3 && tag == 'b' && bm == t.bm && bn == t.bn;
+      }
+      if (take) {
+        best = c;
+        pl.big = true;
+        pl.bt = t;
+      }
+    }
+  }
   return pl;
 }
 
@@ -1320,7 +1682,7 @@ Plan make_plan(const GemmDesc& d) {
 int gemm_split_plan(const GemmDesc& d, size_t* ws_bytes) {
   *ws_bytes = 0;
   const Plan pl = make_plan(d);
-  if (!pl.pipelined) return 1;
+  if (!pl.pipelined || pl.big) return 1;
   const long long ntiles =
       (long long)((d.M + pl.t.bm - 1) / pl.t.bm) * ((d.N + pl.t.bn - 1) / pl.t.bn) * d.batch;
   const int kt = (d.K + 128 / pl.es - 1) / (128 / pl.es);
@@ -1385,6 +1747,26 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
     kp.splits = d.splits;
     kp.kchunk = (kt + d.splits - 1) / d.splits;
     kp.ws = d.ws;
+  }
+  kp.nt_store = 0;
+  if (pl.big && d.splits <= 1) {
+    // output of at least 8 MB: written past the caches (it does not fit the
+    // L2s and the next kernel streams it from HBM either way)
+    kp.nt_store = (long long)d.batch * d.M * d.N * es >= (8LL << 20) ? 1 : 0;
+    const Tile& b = pl.bt;
+    kp.tiles_n = (d.N + b.bn - 1) / b.bn;
+    if (name) {
+      char buf[96];
+      snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw4_nk_big", bf ? "bf16" : "f16", b.bm, b.bn);
+      *name = buf;
+    }
+    // 128-byte LDS rows (8 full lines per DMA instruction) and two stages:
+    // measured slightly ahead of 64-byte rows with five stages on MI355X
+    if (b.bm == 256 && b.bn == 192)
+      return bf ? launch_nk<256, 192, 2, 2, true, 2, 128>(kp, d.batch, s) : launch_nk<256, 192, 2, 2, false, 2, 128>(kp, d.batch, s);
+    if (b.bm == 256 && b.bn == 128)
+      return bf ? launch_nk<256, 128, 2, 2, true, 3, 128>(kp, d.batch, s) : launch_nk<256, 128, 2, 2, false, 3, 128>(kp, d.batch, s);
+    return bf ? launch_nk<192, 256, 2, 2, true, 5, 64>(kp, d.batch, s) : launch_nk<192, 256, 2, 2, false, 5, 64>(kp, d.batch, s);
   }
   const bool knv = d.bmode == B_KN && bvec;
   if (name) {
