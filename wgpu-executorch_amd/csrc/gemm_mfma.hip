@@ -1397,36 +1397,62 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(KParams p) {
   const int nq = (N + 3) / 4;
   const long long total = (long long)p.batch * M * nq;
   const long long slab = (long long)p.batch * M * N;
+  const bool n4 = (N & 3) == 0;  // rows of whole float4s: one 16-byte load per range
   char* Cb = reinterpret_cast<char*>(p.C);
-  constexpr int ES = DT == DT_F32 ? 4 : 2;
   for (long long q = (long long)blockIdx.x * 256 + threadIdx.x; q < total; q += (long long)gridDim.x * 256) {
     const int n = (int)(q % nq) * 4;
     const long long zm = q / nq;
     const int m = (int)(zm % M), z = (int)(zm / M);
     const long long base = zm * N + n;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int r = 0; r < S; ++r)
+    if (n4) {
+      float4 t[8];  // every range's load in flight before the sum (S <= 8)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < N) v[e] += p.ws[(long long)r * slab + base + e];
+      for (int r = 0; r < 8; ++r)
+        if (r < S) t[r] = *reinterpret_cast<const float4*>(p.ws + (long long)r * slab + base);
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        if (r < S) {
+          v[0] += t[r].x;
+          v[1] += t[r].y;
+          v[2] += t[r].z;
+          v[3] += t[r].w;
+        }
+    } else {
+      for (int r = 0; r < S; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) v[e] += p.ws[(long long)r * slab + base + e];
+    }
     const long long cbase = (long long)z * p.sC + (long long)m * p.ldc + n;
+    uint32_t h[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      if (n + e >= N) continue;
       float x = p.alpha * v[e];
-      if (p.bias_mode == BIAS_ROW) {
-        x += p.beta * (DT == DT_F32 ? reinterpret_cast<const float*>(p.bias)[m] : ld_f32<DT == DT_BF16>(p.bias[m]));
-      } else if (p.bias_mode == BIAS_COL) {
-        x += p.beta *
-             (DT == DT_F32 ? reinterpret_cast<const float*>(p.bias)[n + e] : ld_f32<DT == DT_BF16>(p.bias[n + e]));
+      if (n + e < N) {
+        if (p.bias_mode == BIAS_ROW) {
+          x += p.beta * (DT == DT_F32 ? reinterpret_cast<const float*>(p.bias)[m] : ld_f32<DT == DT_BF16>(p.bias[m]));
+        } else if (p.bias_mode == BIAS_COL) {
+          x += p.beta *
+               (DT == DT_F32 ? reinterpret_cast<const float*>(p.bias)[n + e] : ld_f32<DT == DT_BF16>(p.bias[n + e]));
+        }
       }
       if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
-      if constexpr (DT == DT_F32)
-        reinterpret_cast<float*>(Cb)[cbase + e] = x;
-      else
-        reinterpret_cast<uint16_t*>(Cb)[cbase + e] = st_bits<DT == DT_BF16>(x);
+      h[e] = DT == DT_F32 ? __float_as_uint(x) : (uint32_t)st_bits<DT == DT_BF16>(x);
     }
-    (void)ES;
+    const bool cv = n4 && ((p.ldc & 3) == 0) && ((p.sC & 3) == 0) &&
+                    ((reinterpret_cast<uintptr_t>(p.C) & (4 * (DT == DT_F32 ? 4 : 2) - 1)) == 0);
+    if constexpr (DT == DT_F32) {
+      if (cv) *reinterpret_cast<uint4*>(reinterpret_cast<float*>(Cb) + cbase) = make_uint4(h[0], h[1], h[2], h[3]);
+      else
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) reinterpret_cast<uint32_t*>(Cb)[cbase + e] = h[e];
+    } else {
+      if (cv) *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(Cb) + cbase) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+      else
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) reinterpret_cast<uint16_t*>(Cb)[cbase + e] = (uint16_t)h[e];
+    }
   }
 }
 
@@ -1802,7 +1828,7 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
     kr.batch = d.batch;
     const long long total = (long long)d.batch * d.M * ((d.N + 3) / 4);
     long long grid = (total + 255) / 256;
-    if (grid > 4LL * device_cus()) grid = 4LL * device_cus();
+    if (grid > 64LL * device_cus()) grid = 64LL * device_cus();
     if (dt == DT_F32) hipLaunchKernelGGL(k_splitk_reduce<DT_F32>, dim3((unsigned)grid), dim3(256), 0, s, kr);
     else if (dt == DT_BF16) hipLaunchKernelGGL(k_splitk_reduce<DT_BF16>, dim3((unsigned)grid), dim3(256), 0, s, kr);
     else hipLaunchKernelGGL(k_splitk_reduce<DT_F16>, dim3((unsigned)grid), dim3(256), 0, s, kr);
