@@ -75,7 +75,13 @@ typedef struct {
 /* aten.convolution.default scalar arguments (src/shaders/convolution/
  * index.ts:33-44) plus the clamp of et_vk.conv_with_clamp.default
  * (src/shaders/conv-with-clamp/index.ts:33-46).  Two-element lists are given
- * already expanded (parseHw, src/shaders/convolution/index.ts:46-50). */
+ * already expanded (parseHw, src/shaders/convolution/index.ts:46-50).
+ * `activation` has no counterpart in the reference's operators: it lets a
+ * program runner fold a following elementwise activation into the
+ * convolution's epilogue (conv -> sigmoid -> mul is SiLU); it is applied
+ * after the bias and before the clamp, in float32, before the one rounding. */
+#define WGX_ACT_NONE 0
+#define WGX_ACT_SILU 1
 typedef struct {
   int32_t stride[2];
   int32_t padding[2];
@@ -86,6 +92,7 @@ typedef struct {
   int32_t has_clamp;
   float clamp_min;
   float clamp_max;
+  int32_t activation; /* WGX_ACT_NONE or WGX_ACT_SILU */
 } wgx_conv_args;
 
 typedef struct wgx_ctx wgx_ctx;

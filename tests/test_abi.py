@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(pkg):
 def test_struct_layouts_match_header(pkg):
     W = pkg.wgx
     assert ctypes.sizeof(W.CTensor) == 8 + 4 + 4 + 8 * 8
-    assert ctypes.sizeof(W.CConvArgs) == 4 * 13
+    assert ctypes.sizeof(W.CConvArgs) == 4 * 14  # 13 words of conv arguments + activation
 
 
 @pytest.fixture()

@@ -156,6 +156,43 @@ def test_depthwise_unaligned_views(gpu_ctx, orc, pkg, dtype):
     gpu_ctx.free(by)
 
 
+SILU_CASES = [
+    # x shape, w shape, stride, pad, groups -- one per kernel family
+    ((1, 16, 20, 20), (32, 16, 3, 3), (1, 1), (1, 1), 1),        # implicit-im2col GEMM
+    ((1, 32, 12, 12), (48, 32, 1, 1), (1, 1), (0, 0), 1),        # 1x1: plain GEMM
+    ((1, 128, 40, 40), (256, 128, 3, 3), (2, 2), (1, 1), 1),     # split-K GEMM + reduction
+    ((1, 24, 16, 16), (24, 1, 3, 3), (1, 1), (1, 1), 24),        # depthwise, register kernel (fp16)
+    ((1, 6, 13, 17), (6, 1, 5, 5), (2, 2), (2, 2), 6),           # depthwise, LDS kernel
+    ((1, 8, 12, 12), (8, 1, 3, 3), (1, 1), (2, 2), 8),           # depthwise, generic (dilation 2 below)
+    ((1, 8, 10, 10), (12, 4, 3, 3), (1, 1), (1, 1), 2),          # grouped direct
+]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_conv_silu_epilogue(gpu_ctx, orc, pkg, dtype):
+    """The SiLU epilogue (bias, then x * sigmoid(x), one rounding) on every
+    convolution kernel family, against the fp64 oracle's convolution followed
+    by SiLU in fp64."""
+    W, I = pkg.wgx, pkg.inputs
+    for i, (xs, ws, s, p, g) in enumerate(SILU_CASES):
+        d = (2, 2) if i == 5 else (1, 1)
+        x = round_in(I.uniform(1800 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(1810 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(1820 + i, (ws[0],), -0.5, 0.5), dtype)
+        ref, refa = orc.conv2d_f64(x, w, b, s, p, d, g)
+        tx, tw, tb = gpu_ctx.from_numpy(x, dtype), gpu_ctx.from_numpy(w, dtype), gpu_ctx.from_numpy(b, dtype)
+        ty = gpu_ctx.tensor(dtype, list(ref.shape))
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, tb, list(s), list(p), list(d), False, [0, 0], g, ty, activation=W.ACT_SILU)
+        kernel = gpu_ctx.last_kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        silu = ref / (1.0 + np.exp(-ref))
+        # |d silu / dx| <= 1.1: the convolution's error bound, scaled
+        assert_parity(ty.get_f32(), silu, 1.1 * refa, dtype, ws[1] * ws[2] * ws[3],
+                      f"silu {i} {dtype} {xs}x{ws} {kernel}")
+
+
 CONV_SWEEP = [
     # x shape, w shape, stride, pad, dilation, groups
     ((1, 3, 64, 64), (16, 3, 3, 3), (2, 2), (1, 1), (1, 1), 1),      # stem: K = 27

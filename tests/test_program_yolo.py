@@ -93,15 +93,52 @@ def test_generator_pool_plan_follows_converter_rule(Y):
             assert e0 < s1, "two live tensors share a pool"
 
 
+def _expected_silu_fusions(prog):
+    """conv -> sigmoid -> mul triples recordProgram folds: the two
+    intermediates read by nothing else, and the product not in the pool of
+    the convolution's input (tensors of one pool share its memory)."""
+    vals, chain = prog["values"], prog["chain"]
+    uses = {}
+    for op in chain:
+        for a in op["args"]:
+            for t in _tensor_ids(prog, a):
+                uses[t] = uses.get(t, 0) + 1
+    for t in prog["outputIds"]:
+        uses[t] = uses.get(t, 0) + 1
+    n, k = 0, 0
+    while k + 2 < len(chain):
+        conv, sig, mul = chain[k:k + 3]
+        c = conv["args"][-1]
+        ok = (conv["name"] == "aten.convolution.default" and sig["name"] == "aten.sigmoid.default"
+              and mul["name"] == "aten.mul.Tensor" and sig["args"][0] == c)
+        if ok:
+            s, y = sig["args"][1], mul["args"][2]
+            ok = (sorted(mul["args"][:2]) == sorted([c, s]) and uses.get(c) == 3 and uses.get(s) == 2
+                  and vals[y].get("memObjId") != vals[conv["args"][0]].get("memObjId"))
+        if ok:
+            n += 1
+            k += 3
+        else:
+            k += 1
+    return n
+
+
 @needs_node
 def test_js_host_records_the_program(Y, tmp_path):
     Y.write(str(tmp_path), img=160)
-    r = subprocess.run([NODE, RUNNER, str(tmp_path), "--device", "-1", "--record-only"],
-                       capture_output=True, text=True, timeout=120)
-    assert r.returncode == 0, r.stderr
-    res = json.loads(r.stdout.strip().splitlines()[-1])
     prog = json.load(open(tmp_path / "program.json"))
-    assert res["ops"] == len(prog["chain"]) and res["commands"] >= len(prog["chain"])
+    res = {}
+    for fuse in (True, False):
+        cmd = [NODE, RUNNER, str(tmp_path), "--device", "-1", "--record-only"] + ([] if fuse else ["--no-fuse"])
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        res[fuse] = json.loads(r.stdout.strip().splitlines()[-1])
+        assert res[fuse]["ops"] == len(prog["chain"])
+    assert res[False]["commands"] >= len(prog["chain"])
+    # every conv -> sigmoid -> mul the rule allows is one launch instead of three
+    n = _expected_silu_fusions(prog)
+    assert n > 0
+    assert res[False]["commands"] - res[True]["commands"] == 2 * n
 
 
 # ------------------------------------------------------------ evaluator pins
@@ -175,14 +212,15 @@ def test_evaluator_ops_match_torch(orc):
 
 
 # ------------------------------------------------------------ GPU runs
-def _gpu_vs_cpu(Y, tmp_path, img):
+def _gpu_vs_cpu(Y, tmp_path, img, fuse=True):
     from oracle import program_eval
 
     Y.write(str(tmp_path), img=img)
     out = tmp_path / "out.bin"
-    print(f"[yolo program] img={img}: running on GPU 0 through Node", flush=True)
+    print(f"[yolo program] img={img} fuse={fuse}: running on GPU 0 through Node", flush=True)
     r = subprocess.run([NODE, RUNNER, str(tmp_path), "--device", "0", "--warmup", "1", "--reps", "3",
-                        "--out", str(out)], capture_output=True, text=True, timeout=180)
+                        "--out", str(out)] + ([] if fuse else ["--no-fuse"]),
+                       capture_output=True, text=True, timeout=180)
     assert r.returncode == 0, r.stderr[-3000:]
     gpu = np.fromfile(out, dtype=np.float16).astype(np.float64)
     prog = json.load(open(tmp_path / "program.json"))
@@ -206,6 +244,12 @@ def _gpu_vs_cpu(Y, tmp_path, img):
 @pytest.mark.gpu
 def test_yolo_program_gpu_matches_cpu_160(Y, orc, tmp_path):
     _gpu_vs_cpu(Y, tmp_path, 160)
+
+
+@needs_node
+@pytest.mark.gpu
+def test_yolo_program_gpu_matches_cpu_160_unfused(Y, orc, tmp_path):
+    _gpu_vs_cpu(Y, tmp_path, 160, fuse=False)
 
 
 @needs_node

@@ -23,6 +23,7 @@ struct DcParams {
   void* y;
   int B, IC, IH, IW, OC, OH, OW, KH, KW, sH, sW, pH, pW, dH, dW, groups;
   int has_clamp;
+  int act;
   float cmin, cmax;
   long long total;
 };
@@ -94,6 +95,7 @@ __global__ __launch_bounds__(256) void k_direct(DcParams p) {
       }
     }
   }
+  acc = apply_act(p.act, acc);
   if (p.has_clamp) acc = fminf(fmaxf(acc, p.cmin), p.cmax);
   stv<DT>(p.y, i, acc);
 }
@@ -134,6 +136,7 @@ hipError_t launch_direct_conv(const DirectConvDesc& d, hipStream_t s, std::strin
   p.dW = d.dW;
   p.groups = d.groups;
   p.has_clamp = d.has_clamp;
+  p.act = d.act;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
   p.total = (long long)d.B * d.OC * d.OH * d.OW;

@@ -58,6 +58,7 @@ struct DwParams {
   int in_rows;  // LDS rows per band
   int lw;       // LDS row width
   int has_clamp;
+  int act;
   float cmin, cmax;
 };
 
@@ -149,6 +150,7 @@ __global__ __launch_bounds__(NT) void k_depthwise(DwParams p) {
       for (int kh = 0; kh < KH; ++kh)
         for (int kw = 0; kw < KW; ++kw) acc += src[kh * p.dH * p.lw + kw * p.dW] * wp[kh * KW + kw];
     }
+    acc = apply_act(p.act, acc);
     if (p.has_clamp) acc = fminf(fmaxf(acc, p.cmin), p.cmax);
     stv<DT>(p.y, ((long long)(plane0 + pp) * p.OH + oh0 + orow) * p.OW + ow, acc);
   }
@@ -184,6 +186,7 @@ struct DwFast {
   FastDiv fd_items;  // OH * segs (items of one whole plane)
   FastDiv fd_segs;   // segs
   int has_clamp;
+  int act;
   float cmin, cmax;
 };
 
@@ -382,6 +385,7 @@ __global__ __launch_bounds__(NT) void k_dw_fast(DwFast p) {
 #pragma unroll
     for (int o = 0; o < OV; ++o) {
       float v = acc[o];
+      v = apply_act(p.act, v);
       if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
       h[o] = to_bits<DT>(v);
     }
@@ -443,6 +447,7 @@ struct DwReg {
   long long units;
   unsigned long long x_bytes, y_bytes;
   int has_clamp;
+  int act;
   float cmin, cmax;
 };
 
@@ -614,6 +619,7 @@ __global__ __launch_bounds__(64) void k_dw_reg(DwReg p) {
 #pragma unroll
     for (int o = 0; o < OV; ++o) {
       float v = acc[r][o];
+      v = apply_act(p.act, v);
       if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
       h[o] = __builtin_bit_cast(uint16_t, (_Float16)v);
     }
@@ -684,6 +690,7 @@ bool plan_reg(const DwDesc& d, DwReg& p, int& ov, int& R, long long& blocks) {
   p.x_bytes = (unsigned long long)nplanes * d.IH * d.IW * 2;
   p.y_bytes = (unsigned long long)nplanes * d.OH * d.OW * 2;
   p.has_clamp = d.has_clamp;
+  p.act = d.act;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
   blocks = p.units;
@@ -834,6 +841,7 @@ bool plan_fast(const DwDesc& d, DwFast& p, int& ov, int& blocks, size_t& lds) {
   p.fd_items = make_fastdiv((uint32_t)(d.OH * segs));
   p.fd_segs = make_fastdiv((uint32_t)segs);
   p.has_clamp = d.has_clamp;
+  p.act = d.act;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
   return (long long)p.ppb * d.IH * d.IW < (1LL << 30);
@@ -879,6 +887,7 @@ hipError_t launch_depthwise(const DwDesc& d, hipStream_t s, std::string* name) {
   p.dH = d.dH;
   p.dW = d.dW;
   p.has_clamp = d.has_clamp;
+  p.act = d.act;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
   p.nplanes = d.B * d.C;

@@ -36,6 +36,7 @@ struct KParams {
   int bias_mode;
   float alpha, beta;
   int has_clamp;
+  int act;
   float cmin, cmax;
   ConvGeom g;
   int tiles_n;
@@ -263,6 +264,7 @@ __global__ __launch_bounds__(NT) void k_sgemm(KParams p) {
       if (gn >= N) continue;
       float v = p.alpha * acc[i][j] + rowb;
       if (p.bias_mode == BIAS_COL) v += p.beta * p.bias[gn];
+      v = apply_act(p.act, v);
       if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
       C[gm * p.ldc + gn] = v;
     }
@@ -308,6 +310,7 @@ hipError_t launch_gemm_f32(const GemmDesc& d, hipStream_t s, std::string* name) 
   kp.alpha = d.alpha;
   kp.beta = d.beta;
   kp.has_clamp = d.has_clamp;
+  kp.act = d.act;
   kp.cmin = d.cmin;
   kp.cmax = d.cmax;
   kp.g = d.g;

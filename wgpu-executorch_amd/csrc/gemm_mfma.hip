@@ -61,6 +61,7 @@ struct KParams {
   int bias_mode;
   float alpha, beta;
   int has_clamp;
+  int act;
   float cmin, cmax;
   ConvGeom g;
   int tiles_n;
@@ -511,6 +512,7 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
+            x = apply_act(p.act, x);
             if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
             v[e] = x;
           }
@@ -1088,6 +1090,7 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
+            x = apply_act(p.act, x);
             if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
             if constexpr (DT == DT_F32) h[e] = __float_as_uint(x);
             else h[e] = st_bits<DT == DT_BF16>(x);
@@ -1332,6 +1335,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
+                x = apply_act(p.act, x);
                 if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
                 h[e] = st_bits<BF>(x);
               }
@@ -1437,6 +1441,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(KParams p) {
                (DT == DT_F32 ? reinterpret_cast<const float*>(p.bias)[n + e] : ld_f32<DT == DT_BF16>(p.bias[n + e]));
         }
       }
+      x = apply_act(p.act, x);
       if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
       h[e] = DT == DT_F32 ? __float_as_uint(x) : (uint32_t)st_bits<DT == DT_BF16>(x);
     }
@@ -1743,6 +1748,7 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
   kp.alpha = d.alpha;
   kp.beta = d.beta;
   kp.has_clamp = d.has_clamp;
+  kp.act = d.act;
   kp.cmin = d.cmin;
   kp.cmax = d.cmax;
   kp.g = d.g;

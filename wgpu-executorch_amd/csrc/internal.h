@@ -10,6 +10,13 @@
 
 namespace wgx {
 
+// Epilogue activation of a convolution: v = act(acc + bias), then clamp.
+// SiLU is x * sigmoid(x) = x / (1 + e^-x), in float32 before the one
+// rounding to the storage type.
+__device__ __forceinline__ float apply_act(int act, float x) {
+  return act == WGX_ACT_SILU ? x / (1.0f + __expf(-x)) : x;
+}
+
 // Passing this stream to a launch_* function selects the kernel, fills *name
 // and performs one-time kernel set-up (LDS attributes) without launching.
 inline hipStream_t describe_only() { return reinterpret_cast<hipStream_t>(~uintptr_t(0)); }
@@ -47,6 +54,7 @@ struct GemmDesc {
   int bias_mode;
   float alpha, beta;
   int has_clamp;
+  int act;  // WGX_ACT_*: applied after the bias, before the clamp
   float cmin, cmax;
   int bmode;
   ConvGeom g;
@@ -80,6 +88,7 @@ struct DwDesc {
   const void* bias;
   void* y;
   int has_clamp;
+  int act;  // WGX_ACT_*: applied after the bias, before the clamp
   float cmin, cmax;
 };
 hipError_t launch_depthwise(const DwDesc& d, hipStream_t s, std::string* name);
@@ -93,6 +102,7 @@ struct DirectConvDesc {
   const void* bias;
   void* y;
   int has_clamp;
+  int act;  // WGX_ACT_*: applied after the bias, before the clamp
   float cmin, cmax;
 };
 hipError_t launch_direct_conv(const DirectConvDesc& d, hipStream_t s, std::string* name);

@@ -561,6 +561,9 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
   if (B * IC * IH * IW > INT32_MAX || B * OC * OH * OW > INT32_MAX || numel(weight) > INT32_MAX)
     return c->fail(WGX_ERR_INVALID, "convolution: tensors above 2^31 elements are not supported");
   const int has_clamp = args->has_clamp ? 1 : 0;
+  if (args->activation != WGX_ACT_NONE && args->activation != WGX_ACT_SILU)
+    return c->fail(WGX_ERR_INVALID, "convolution: unknown activation %d", (int)args->activation);
+  const int act = args->activation;
   const float cmin = args->clamp_min, cmax = args->clamp_max;
 
   const bool depthwise = !args->transposed && groups == OC && IC == OC && weight->shape[1] == 1;
@@ -588,6 +591,7 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
     d.bias = bias ? bias->data : nullptr;
     d.y = out->data;
     d.has_clamp = has_clamp;
+    d.act = act;
     d.cmin = cmin;
     d.cmax = cmax;
     e = launch_depthwise(d, c->dry(), &name);
@@ -618,6 +622,7 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
     d.alpha = 1.0f;
     d.beta = 1.0f;
     d.has_clamp = has_clamp;
+    d.act = act;
     d.cmin = cmin;
     d.cmax = cmax;
     d.g = geom;
@@ -665,6 +670,7 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
   d.bias = bias ? bias->data : nullptr;
   d.y = out->data;
   d.has_clamp = has_clamp;
+  d.act = act;
   d.cmin = cmin;
   d.cmax = cmax;
   e = launch_direct_conv(d, c->dry(), &name);

@@ -302,6 +302,7 @@ napi_value record_conv2d(napi_env env, napi_callback_info info) {
   ca.has_clamp = i32(env, prop(env, o, "hasClamp"));
   ca.clamp_min = (float)num(env, prop(env, o, "clampMin"));
   ca.clamp_max = (float)num(env, prop(env, o, "clampMax"));
+  ca.activation = i32(env, prop(env, o, "activation"));  // absent: 0, no activation
   if (!ok(env, c, wgx_record_conv2d(c, &tin, &tw, has_bias ? &tb : nullptr, &ca, &to))) return nullptr;
   return undefined(env);
 }

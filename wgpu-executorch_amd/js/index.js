@@ -250,8 +250,9 @@ class WgpuExecutionContext {
    * allocation (256-byte aligned offsets) and constants into one weights
    * allocation, instead of one buffer per pool / per constant.
    */
-  recordProgram(program, weights, args) {
+  recordProgram(program, weights, args, options) {
     this._assertNotDestroyed();
+    const fuse = !(options && options.fuse === false);
     const numInputs = program.inputIds.length;
     const numOutputs = program.outputIds.length;
     if (args.length !== numInputs + numOutputs) {
@@ -319,7 +320,15 @@ class WgpuExecutionContext {
       this.copy(src, dst);
     }
 
-    for (const op of program.chain) {
+    const fused = fuse ? siluFusions(program, tensors) : new Map();
+    for (let k = 0; k < program.chain.length; k++) {
+      const f = fused.get(k);
+      if (f !== undefined) {  // conv -> sigmoid -> mul as one convolution with the SiLU epilogue
+        this.recordShader(shaders.convolutionSilu, f);
+        k += 2;
+        continue;
+      }
+      const op = program.chain[k];
       const shader = shaderRegistry[op.name];
       if (!shader) throw new Error(`program: unknown operator '${op.name}'`);
       this.recordShader(shader, resolveArgs(op, program.values, tensors));
@@ -394,6 +403,55 @@ function resolveArgs(op, values, tensors) {
         return undefined;
     }
   });
+}
+
+// ------------------------------------------------------------------ graph-level fusion
+
+/**
+ * SiLU after a convolution, as exported graphs spell it: conv -> c,
+ * sigmoid(c) -> s, mul(c, s) -> y, three consecutive ops.  When c and s are
+ * read by nothing else (and are not program outputs) the convolution can
+ * write SiLU(conv) straight into y, one launch instead of three and two
+ * feature-map round trips fewer.  Not when y's memory overlaps the
+ * convolution's input, weight or bias: a memory plan may give y the space of
+ * an input that is dead after the convolution, and the fused launch would
+ * then overwrite data it still reads.  Returns chain index -> resolved
+ * arguments of the fused convolution.
+ */
+function siluFusions(program, tensors) {
+  const { chain, values } = program;
+  const uses = new Map();
+  const note = (id) => uses.set(id, (uses.get(id) || 0) + 1);
+  for (const op of chain) {
+    for (const a of op.args) {
+      const v = values[a];
+      if (!v) continue;
+      if (v.type === 'tensor') note(a);
+      else if (v.type === 'tensorlist') v.items.forEach(note);
+    }
+  }
+  for (const id of program.outputIds) note(id);
+  const overlaps = (a, b) => a.buffer.ptr < b.buffer.ptr + b.byteLength && b.buffer.ptr < a.buffer.ptr + a.byteLength;
+  const out = new Map();
+  for (let k = 0; k + 2 < chain.length; k++) {
+    const conv = chain[k], sig = chain[k + 1], mul = chain[k + 2];
+    if (conv.name !== 'aten.convolution.default' || sig.name !== 'aten.sigmoid.default' ||
+        mul.name !== 'aten.mul.Tensor' || sig.args.length !== 2 || mul.args.length !== 3) continue;
+    const c = conv.args[conv.args.length - 1], s = sig.args[1], y = mul.args[2];
+    if (sig.args[0] !== c || !((mul.args[0] === c && mul.args[1] === s) || (mul.args[0] === s && mul.args[1] === c))) continue;
+    if (uses.get(c) !== 3 || uses.get(s) !== 2) continue;
+    const tc = tensors.get(c), ty = tensors.get(y);
+    if (!tc || !ty || ty.dtype !== tc.dtype || ty.shape.length !== tc.shape.length ||
+        ty.shape.some((d, i) => d !== tc.shape[i])) continue;
+    const reads = [0, 1, 2].map((i) => conv.args[i]).filter((i) => values[i] && values[i].type === 'tensor')
+      .map((i) => tensors.get(i));
+    if (reads.some((t) => !t || overlaps(t, ty))) continue;
+    const args = resolveArgs(conv, values, tensors);
+    args[args.length - 1] = ty;
+    out.set(k, args);
+    k += 2;
+  }
+  return out;
 }
 
 // ------------------------------------------------------------------ operators

@@ -14,14 +14,15 @@
  *                    (HIP events on the queue)
  * and, with --out, writes the output tensor's bytes after the timed frames.
  * --record-only validates and records the program without running it (it
- * works on the host-only device -1).
+ * works on the host-only device -1).  --no-fuse records every op of the chain
+ * as it stands (no conv -> sigmoid -> mul folding).
  */
 const fs = require('fs');
 const path = require('path');
 const W = require('./index.js');
 
 function parseArgs(argv) {
-  const a = { dir: null, device: 0, warmup: 5, reps: 50, out: null, recordOnly: false };
+  const a = { dir: null, device: 0, warmup: 5, reps: 50, out: null, recordOnly: false, fuse: true };
   for (let i = 0; i < argv.length; i++) {
     const k = argv[i];
     if (k === '--device') a.device = Number(argv[++i]);
@@ -29,6 +30,7 @@ function parseArgs(argv) {
     else if (k === '--reps') a.reps = Number(argv[++i]);
     else if (k === '--out') a.out = argv[++i];
     else if (k === '--record-only') a.recordOnly = true;
+    else if (k === '--no-fuse') a.fuse = false;
     else a.dir = k;
   }
   if (!a.dir) throw new Error('usage: node run_program.js DIR [--device N] [--warmup W] [--reps R] [--out FILE]');
@@ -51,7 +53,7 @@ async function main() {
   const output = ctx.tensor(outV.dtype, outV.shape);
 
   const t0 = process.hrtime.bigint();
-  ctx.recordProgram(program, weights, [input, output]);
+  ctx.recordProgram(program, weights, [input, output], { fuse: args.fuse });
   const recordMs = Number(process.hrtime.bigint() - t0) / 1e6;
   if (args.recordOnly) {
     console.log(JSON.stringify({ record_ms: recordMs, commands: ctx.commandCount, ops: program.chain.length }));

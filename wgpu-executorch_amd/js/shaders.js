@@ -118,8 +118,10 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
   };
 
   // ---------------------------------------------------------------- convolution (src/shaders/convolution/index.ts:58-310)
+  // activation: 0 none, 1 SiLU folded into the epilogue (recordProgram's
+  // conv -> sigmoid -> mul fusion; the reference operators never pass it)
   function recordConv(name, ctx, inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding,
-    groups, outTensor, clampMin, clampMax) {
+    groups, outTensor, clampMin, clampMax, activation) {
     if (!isFloatPair(inTensor) || weight.dtype !== inTensor.dtype || outTensor.dtype !== inTensor.dtype) {
       throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
     }
@@ -166,8 +168,20 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
       transposed: transposed ? 1 : 0, groups, hasClamp: hasClamp ? 1 : 0,
       clampMin: clampMin === undefined ? -Infinity : clampMin,
       clampMax: clampMax === undefined ? Infinity : clampMax,
+      activation: activation || 0,
     }, outTensor._c());
   }
+
+  /** aten.convolution.default followed by SiLU (x * sigmoid(x)) in one launch. */
+  const convolutionSilu = {
+    name: 'wgx.convolution_silu',
+    code: { all: 'the convolution kernels with the SiLU epilogue enabled' },
+    recordIn(ctx, args) {
+      const [inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding, groups, outTensor] = args;
+      recordConv('aten.convolution.default', ctx, inTensor, weight, bias, stride, padding, dilation, transposed,
+        outputPadding, groups, outTensor, undefined, undefined, 1);
+    },
+  };
 
   const convolution = {
     name: 'aten.convolution.default',
@@ -345,7 +359,7 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
   return {
     add, sub, mul, sigmoid, relu, hardswish,
     mm, addmm, linear, bmm,
-    convolution, convWithClamp, maxPool2d,
+    convolution, convWithClamp, convolutionSilu, maxPool2d,
     upsampleNearest2d,
     cat, splitWithSizesCopy,
     viewCopy: flatCopy('aten.view_copy.default'),

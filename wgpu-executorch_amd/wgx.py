@@ -55,7 +55,10 @@ class CConvArgs(ctypes.Structure):
                 ("dilation", ctypes.c_int32 * 2), ("output_padding", ctypes.c_int32 * 2),
                 ("transposed", ctypes.c_int32), ("groups", ctypes.c_int32),
                 ("has_clamp", ctypes.c_int32), ("clamp_min", ctypes.c_float),
-                ("clamp_max", ctypes.c_float)]
+                ("clamp_max", ctypes.c_float), ("activation", ctypes.c_int32)]
+
+
+ACT_NONE, ACT_SILU = 0, 1
 
 
 _LIB = None
@@ -285,7 +288,7 @@ class Context:
 
     def convolution(self, x: Tensor, w: Tensor, bias: Optional[Tensor], stride=(1, 1),
                     padding=(0, 0), dilation=(1, 1), transposed=False, output_padding=(0, 0),
-                    groups=1, out: Optional[Tensor] = None, clamp=None) -> "Context":
+                    groups=1, out: Optional[Tensor] = None, clamp=None, activation: int = ACT_NONE) -> "Context":
         def hw(v):
             v = list(v) if isinstance(v, (list, tuple)) else [v]
             if len(v) == 1:
@@ -304,6 +307,7 @@ class Context:
             a.has_clamp = 1
             a.clamp_min = -np.inf if clamp[0] is None else float(clamp[0])
             a.clamp_max = np.inf if clamp[1] is None else float(clamp[1])
+        a.activation = int(activation)
         cx, cw, co = x.c(), w.c(), out.c()
         cb = bias.c() if bias is not None else None
         self._check(lib().wgx_record_conv2d(self.h, ctypes.byref(cx), ctypes.byref(cw),
