@@ -86,3 +86,107 @@ describe('WgpuExecutionContext.recordProgram()', () => {
       { type: 'tensor' }, { type: 'tensor' }, { type: 'tensorlist', items: [1] }], tensors)).toThrow(/tensorlist item 1 is not a tensor/);
   });
 });
+
+// ------------------------------------------------------------ zero-copy cat / split / view_copy
+const T = (shape, extra) => Object.assign({ type: 'tensor', shape, dtype: 'float32' }, extra || {});
+const L = (items) => ({ type: 'list', items });
+const S = (value) => ({ type: 'scalar', value });
+const TL = (items) => ({ type: 'tensorlist', items });
+const add = (a, b, alpha, out) => ({ name: 'aten.add.Tensor', args: [a, b, alpha, out] });
+const cat = (list, dim, out) => ({ name: 'aten.cat.default', args: [list, dim, out] });
+const split = (x, sizes, dim, outs) => ({ name: 'aten.split_with_sizes_copy.default', args: [x, sizes, dim, outs] });
+const elidedOf = (p) => [...W._planViews(p).elided].sort((a, b) => a - b);
+
+// x [1,4,2,2] -> t = x + x -> split [p(1ch), q(3ch)] -> r = q + q ->
+// y = cat[r, p] (dim 1) and z = cat[p, r] (p, r in two cats: one copies) ->
+// out = y + z
+function viewProgram() {
+  return {
+    version: '1',
+    chain: [
+      add(0, 0, 1, 2),
+      split(2, 3, 4, 5),
+      add(7, 7, 1, 8),
+      cat(9, 1, 10),
+      cat(11, 1, 12),
+      add(10, 12, 1, 13),
+    ],
+    values: [
+      T([1, 4, 2, 2], { memObjId: 0 }), S(1), T([1, 4, 2, 2], { memObjId: 1 }),
+      L([1, 3]), S(1), TL([6, 7]), T([1, 1, 2, 2], { memObjId: 2 }), T([1, 3, 2, 2], { memObjId: 3 }),
+      T([1, 3, 2, 2], { memObjId: 1 }), TL([8, 6]), T([1, 4, 2, 2], { memObjId: 0 }),
+      TL([6, 8]), T([1, 4, 2, 2], { memObjId: 4 }), T([1, 4, 2, 2], { memObjId: 5 }),
+    ],
+    inputIds: [0],
+    outputIds: [13],
+    memoryPlan: { pools: [0, 1, 2, 3, 4, 5].map((id) => ({ id, size: 64 })) },
+  };
+}
+
+describe('recordProgram views', () => {
+  it('ties a split and the first cat; the second cat of the same pieces copies', () => {
+    const p = viewProgram();
+    expect(elidedOf(p)).toEqual([1, 3]);
+    const plan = W._planViews(p);
+    // y = [r | p], t = [p | q]: r and q share no bytes with p in either
+    const at = (id) => plan.place.get(id).off;
+    expect(at(8) - at(10)).toEqual(0);
+    expect(at(6) - at(10)).toEqual(48);
+    expect(at(6) - at(2)).toEqual(0);
+    expect(at(7) - at(2)).toEqual(16);
+    expect(plan.place.has(0) || plan.place.has(13)).toBe(false);
+  });
+  it('rejects a cat that repeats a piece, outputs, inputs and non-leading dimensions', () => {
+    const rep = viewProgram();
+    rep.chain = [add(0, 0, 1, 6), { name: 'aten.cat.default', args: [5, 4, 13] }, add(13, 13, 1, 12)];
+    rep.values[5] = TL([6, 6]);
+    rep.values[6] = T([1, 2, 2, 2], { memObjId: 2 });
+    rep.outputIds = [12];
+    expect(elidedOf(rep)).toEqual([]);
+    rep.values[5] = TL([6, 3]);
+    rep.values[3] = T([1, 2, 2, 2]);
+    rep.chain.splice(1, 0, add(0, 0, 1, 3));
+    expect(elidedOf(rep)).toEqual([2]);
+    const out = viewProgram();
+    out.outputIds = [10];
+    expect(elidedOf(out)).toEqual([1]);
+    const inp = { version: '1', chain: [add(4, 4, 2, 5), cat(1, 2, 3), add(3, 3, 2, 6)],
+      values: [T([1, 2, 2, 2]), TL([0, 5]), S(1), T([1, 4, 2, 2]), T([1, 2, 2, 2]), T([1, 2, 2, 2]), T([1, 4, 2, 2])],
+      inputIds: [0, 4], outputIds: [6], memoryPlan: { pools: [] } };
+    expect(elidedOf(inp)).toEqual([]);
+    inp.chain.unshift(add(4, 4, 2, 0));
+    inp.inputIds = [4];
+    expect(elidedOf(inp)).toEqual([2]);
+    const deep = { version: '1',
+      chain: [add(0, 0, 1, 2), add(0, 0, 1, 3), cat(4, 5, 6), add(6, 6, 1, 7)],
+      values: [T([1, 2, 3]), S(1), T([1, 2, 3]), T([1, 2, 3]), TL([2, 3]), S(2), T([1, 2, 6]), T([1, 2, 6])],
+      inputIds: [0], outputIds: [7], memoryPlan: { pools: [] } };
+    expect(elidedOf(deep)).toEqual([]);
+    deep.values[5] = S(1);
+    deep.values[6] = T([1, 4, 3]);
+    deep.values[7] = T([1, 4, 3]);
+    expect(elidedOf(deep)).toEqual([2]);
+    deep.values[5] = S(-2);
+    expect(elidedOf(deep)).toEqual([2]);
+  });
+  it('runs split/cat chains with and without views', async () => {
+    const x = new Float32Array(16).map((_, i) => i - 5.5);
+    const t = x.map((v) => 2 * v);
+    const p = t.slice(0, 4), q = t.slice(4);
+    const r = q.map((v) => 2 * v);
+    const y = [...r, ...p], z = [...p, ...r];
+    const want = y.map((v, i) => v + z[i]);
+    for (const views of [true, false]) {
+      const ctx = new WgpuExecutionContext(await setupGPU());
+      const xin = ctx.tensor('float32', [1, 4, 2, 2]).setData(x);
+      const out = ctx.tensor('float32', [1, 4, 2, 2]);
+      ctx.recordProgram(viewProgram(), weights, [xin, out], { views });
+      for (let rep = 0; rep < 2; rep++) {
+        ctx.submit();
+        await ctx.sync();
+        await expectTensorClose(W, out, want);
+      }
+      ctx.destroy();
+    }
+  }, { gpu: true });
+});

@@ -253,6 +253,7 @@ class WgpuExecutionContext {
   recordProgram(program, weights, args, options) {
     this._assertNotDestroyed();
     const fuse = !(options && options.fuse === false);
+    const useViews = !(options && options.views === false);
     const numInputs = program.inputIds.length;
     const numOutputs = program.outputIds.length;
     if (args.length !== numInputs + numOutputs) {
@@ -280,11 +281,24 @@ class WgpuExecutionContext {
     });
     const constSlab = constBytes > 0 ? this.storageBuffer(constBytes) : null;
 
+    // zero-copy cat / split / view_copy groups -> one slab of their own
+    const views = useViews ? planViews(program) : { place: new Map(), groupBytes: new Map(), elided: new Set() };
+    const groupOffset = new Map();
+    let groupBytes = 0;
+    for (const [root, bytes] of views.groupBytes) {
+      groupOffset.set(root, groupBytes);
+      groupBytes += align(Math.max(4, bytes));
+    }
+    const groupSlab = groupBytes > 0 ? this.storageBuffer(groupBytes) : null;
+
     const tensors = new Map();
     program.values.forEach((v, i) => {
       if (v.type !== 'tensor') return;
       let buffer;
-      if (v.weightsOffset !== undefined && v.weightsLength !== undefined) {
+      if (views.place.has(i)) {
+        const p = views.place.get(i);
+        buffer = groupSlab.view(groupOffset.get(p.root) + p.off, valueBytes(v));
+      } else if (v.weightsOffset !== undefined && v.weightsLength !== undefined) {
         buffer = constSlab.view(constOffset.get(i), Math.max(4, Math.ceil(v.weightsLength / 4) * 4));
       } else if (v.memObjId !== undefined) {
         if (!poolOffset.has(v.memObjId)) {
@@ -312,6 +326,35 @@ class WgpuExecutionContext {
       native.write(this._device._h, constSlab.ptr, staging.buffer, 0, constBytes);
     }
 
+    let fused = new Map();
+    if (fuse) {
+      const triples = siluTriples(program);
+      // A memory plan may give the product y the space of an input of the
+      // convolution that is dead after it (the unfused mul reads only c and
+      // s).  The fused launch would then overwrite data it still reads, so
+      // such a y, when it is not part of a view group, moves to memory of
+      // its own: one buffer for all of them.
+      const moved = triples.filter((t) => !views.place.has(t.y) &&
+        convReads(program, t.k, tensors).some((r) => overlaps(r, tensors.get(t.y))));
+      const movedBytes = moved.reduce((n, t) => n + align(Math.max(4, tensors.get(t.y).byteLength)), 0);
+      if (movedBytes > 0) {
+        const slab = this.storageBuffer(movedBytes);
+        let at = 0;
+        for (const t of moved) {
+          const ty = tensors.get(t.y);
+          tensors.set(t.y, this.tensor(ty.dtype, ty.shape, slab.view(at, ty.byteLength)));
+          at += align(Math.max(4, ty.byteLength));
+        }
+      }
+      for (const t of triples) {
+        const ty = tensors.get(t.y);
+        if (convReads(program, t.k, tensors).some((r) => overlaps(r, ty))) continue;
+        const fargs = resolveArgs(program.chain[t.k], program.values, tensors);
+        fargs[fargs.length - 1] = ty;
+        fused.set(t.k, fargs);
+      }
+    }
+
     for (let i = 0; i < numInputs; i++) {
       const src = args[i];
       const dst = tensors.get(program.inputIds[i]);
@@ -320,8 +363,8 @@ class WgpuExecutionContext {
       this.copy(src, dst);
     }
 
-    const fused = fuse ? siluFusions(program, tensors) : new Map();
     for (let k = 0; k < program.chain.length; k++) {
+      if (views.elided.has(k)) continue;  // its output already is its inputs' bytes
       const f = fused.get(k);
       if (f !== undefined) {  // conv -> sigmoid -> mul as one convolution with the SiLU epilogue
         this.recordShader(shaders.convolutionSilu, f);
@@ -407,51 +450,210 @@ function resolveArgs(op, values, tensors) {
 
 // ------------------------------------------------------------------ graph-level fusion
 
-/**
- * SiLU after a convolution, as exported graphs spell it: conv -> c,
- * sigmoid(c) -> s, mul(c, s) -> y, three consecutive ops.  When c and s are
- * read by nothing else (and are not program outputs) the convolution can
- * write SiLU(conv) straight into y, one launch instead of three and two
- * feature-map round trips fewer.  Not when y's memory overlaps the
- * convolution's input, weight or bias: a memory plan may give y the space of
- * an input that is dead after the convolution, and the fused launch would
- * then overwrite data it still reads.  Returns chain index -> resolved
- * arguments of the fused convolution.
- */
-function siluFusions(program, tensors) {
-  const { chain, values } = program;
+function valueBytes(v) {
+  return v.shape.reduce((a, b) => a * b, 1) * DTYPE_BYTESIZE[v.dtype];
+}
+
+function overlaps(a, b) {
+  return a.buffer.ptr < b.buffer.ptr + b.byteLength && b.buffer.ptr < a.buffer.ptr + a.byteLength;
+}
+
+/** How many times each value is read by the chain (program outputs count once). */
+function useCounts(program) {
   const uses = new Map();
   const note = (id) => uses.set(id, (uses.get(id) || 0) + 1);
-  for (const op of chain) {
+  for (const op of program.chain) {
     for (const a of op.args) {
-      const v = values[a];
+      const v = program.values[a];
       if (!v) continue;
       if (v.type === 'tensor') note(a);
       else if (v.type === 'tensorlist') v.items.forEach(note);
     }
   }
   for (const id of program.outputIds) note(id);
-  const overlaps = (a, b) => a.buffer.ptr < b.buffer.ptr + b.byteLength && b.buffer.ptr < a.buffer.ptr + a.byteLength;
-  const out = new Map();
+  return uses;
+}
+
+/** Values an op writes: out-variant operators take their outputs last. */
+function opOutputs(op, values) {
+  const last = op.args[op.args.length - 1];
+  const v = values[last];
+  if (!v) return [];
+  if (v.type === 'tensor') return [last];
+  if (v.type === 'tensorlist') return v.items.slice();
+  return [];
+}
+
+/** The tensors a convolution reads (input, weight, bias). */
+function convReads(program, k, tensors) {
+  const conv = program.chain[k];
+  return [0, 1, 2].map((i) => conv.args[i])
+    .filter((i) => program.values[i] && program.values[i].type === 'tensor')
+    .map((i) => tensors.get(i));
+}
+
+/**
+ * SiLU after a convolution, as exported graphs spell it: conv -> c,
+ * sigmoid(c) -> s, mul(c, s) -> y, three consecutive ops.  When c and s are
+ * read by nothing else (and are not program outputs) the convolution can
+ * write SiLU(conv) straight into y, one launch instead of three and two
+ * feature-map round trips fewer.  Returns the triples as {k, y}: k the
+ * convolution's chain index, y the product.
+ */
+function siluTriples(program) {
+  const { chain, values } = program;
+  const uses = useCounts(program);
+  const out = [];
+  const same = (a, b) => a && b && a.type === 'tensor' && b.type === 'tensor' && a.dtype === b.dtype &&
+    a.shape.length === b.shape.length && a.shape.every((d, i) => d === b.shape[i]);
   for (let k = 0; k + 2 < chain.length; k++) {
     const conv = chain[k], sig = chain[k + 1], mul = chain[k + 2];
     if (conv.name !== 'aten.convolution.default' || sig.name !== 'aten.sigmoid.default' ||
         mul.name !== 'aten.mul.Tensor' || sig.args.length !== 2 || mul.args.length !== 3) continue;
     const c = conv.args[conv.args.length - 1], s = sig.args[1], y = mul.args[2];
     if (sig.args[0] !== c || !((mul.args[0] === c && mul.args[1] === s) || (mul.args[0] === s && mul.args[1] === c))) continue;
-    if (uses.get(c) !== 3 || uses.get(s) !== 2) continue;
-    const tc = tensors.get(c), ty = tensors.get(y);
-    if (!tc || !ty || ty.dtype !== tc.dtype || ty.shape.length !== tc.shape.length ||
-        ty.shape.some((d, i) => d !== tc.shape[i])) continue;
-    const reads = [0, 1, 2].map((i) => conv.args[i]).filter((i) => values[i] && values[i].type === 'tensor')
-      .map((i) => tensors.get(i));
-    if (reads.some((t) => !t || overlaps(t, ty))) continue;
-    const args = resolveArgs(conv, values, tensors);
-    args[args.length - 1] = ty;
-    out.set(k, args);
+    if (uses.get(c) !== 3 || uses.get(s) !== 2 || !same(values[c], values[y])) continue;
+    out.push({ k, y });
     k += 2;
   }
   return out;
+}
+
+/**
+ * Zero-copy concatenation, split and view_copy.  When every dimension
+ * before the cat (split) dimension has size 1, a concatenation is its inputs
+ * laid end to end and each piece of a split is a contiguous byte range of
+ * its input; a view_copy is its input's bytes unchanged.  If the producers of
+ * the pieces write straight into the whole, such an op has nothing left to
+ * do.  Each op ties its tensors together at fixed byte offsets (a union-find
+ * with offsets); tied tensors form a group that gets memory of its own,
+ * outside the memory-plan pools, whose sharing assumes the copies happen.
+ * An op is taken only if, with it, every group still has exactly one writer
+ * per byte (a tensor written by an op that still runs) and every tensor's
+ * bytes are all written; otherwise its ties are undone and it runs as a copy.
+ * Program inputs, outputs and constants never join a group.
+ *
+ * Returns place: value -> {root, off} (byte offset within the group),
+ * groupBytes: root -> group size, elided: chain indices with nothing to do.
+ */
+function planViews(program) {
+  const { chain, values } = program;
+  const producer = new Map();
+  chain.forEach((op, k) => {
+    for (const id of opOutputs(op, values)) producer.set(id, producer.has(id) ? -1 : k);
+  });
+  const fixed = new Set([...program.inputIds, ...program.outputIds]);
+  const movable = (id) => {
+    const v = values[id];
+    return v && v.type === 'tensor' && v.weightsOffset === undefined && !fixed.has(id) &&
+      producer.get(id) >= 0 && valueBytes(v) > 0;
+  };
+
+  let parent = new Map(), offset = new Map();
+  const find = (id) => {
+    let d = 0;
+    while (parent.has(id)) { d += offset.get(id); id = parent.get(id); }
+    return [id, d];
+  };
+  // a's bytes start `delta` bytes after b's
+  const tie = (a, b, delta) => {
+    const [ra, da] = find(a), [rb, db] = find(b);
+    if (ra === rb) return da === db + delta;
+    parent.set(ra, rb);
+    offset.set(ra, db + delta - da);
+    return true;
+  };
+  const members = new Set();
+  const elided = new Set();
+  const consistent = () => {
+    const groups = new Map();
+    for (const id of members) {
+      const [r, d] = find(id);
+      if (!groups.has(r)) groups.set(r, []);
+      groups.get(r).push({ id, lo: d, hi: d + valueBytes(values[id]) });
+    }
+    for (const list of groups.values()) {
+      if (list.some((m) => values[m.id].dtype !== values[list[0].id].dtype)) return false;
+      const writers = list.filter((m) => !elided.has(producer.get(m.id))).sort((a, b) => a.lo - b.lo);
+      for (let i = 1; i < writers.length; i++) if (writers[i].lo < writers[i - 1].hi) return false;
+      for (const m of list) {
+        let at = m.lo;
+        for (const w of writers) {
+          if (w.hi <= at) continue;
+          if (w.lo > at) break;
+          at = w.hi;
+          if (at >= m.hi) break;
+        }
+        if (at < m.hi) return false;
+      }
+    }
+    return true;
+  };
+  // pieces[i] starts at byte offsets[i] of whole, when dims before `dim` are all 1
+  const contiguousPieces = (whole, pieces, dim) => {
+    const w = values[whole];
+    if (!w || w.type !== 'tensor') return null;
+    const d = dim < 0 ? dim + w.shape.length : dim;
+    if (!(d >= 0 && d < w.shape.length) || w.shape.slice(0, d).some((n) => n !== 1)) return null;
+    const offs = [];
+    let at = 0;
+    for (const p of pieces) {
+      const v = values[p];
+      if (!v || v.type !== 'tensor' || v.dtype !== w.dtype) return null;
+      offs.push(at);
+      at += valueBytes(v);
+    }
+    return at === valueBytes(w) ? offs : null;
+  };
+
+  chain.forEach((op, k) => {
+    let ties = null;  // [a, b, delta]: a starts delta bytes after b
+    const a = op.args;
+    if (op.name === 'aten.cat.default' && a.length === 3 && values[a[0]] && values[a[0]].type === 'tensorlist') {
+      const items = values[a[0]].items, y = a[2];
+      const offs = contiguousPieces(y, items, values[a[1]].value);
+      if (offs) ties = items.map((id, i) => [id, y, offs[i]]);
+    } else if (op.name === 'aten.split_with_sizes_copy.default' && a.length === 4 &&
+               values[a[3]] && values[a[3]].type === 'tensorlist') {
+      const items = values[a[3]].items, x = a[0];
+      const offs = contiguousPieces(x, items, values[a[2]].value);
+      if (offs) ties = items.map((id, i) => [id, x, offs[i]]);
+    } else if (op.name === 'aten.view_copy.default' && a.length === 3) {
+      const x = a[0], y = a[2];
+      if (values[x] && values[y] && values[x].type === 'tensor' && values[y].type === 'tensor' &&
+          values[x].dtype === values[y].dtype && valueBytes(values[x]) === valueBytes(values[y])) ties = [[y, x, 0]];
+    }
+    if (!ties || ties.some(([p, q]) => !movable(p) || !movable(q))) return;
+    const saved = [new Map(parent), new Map(offset), new Set(members)];
+    elided.add(k);
+    let ok = true;
+    for (const [p, q, delta] of ties) {
+      members.add(p);
+      members.add(q);
+      if (!tie(p, q, delta)) { ok = false; break; }
+    }
+    if (!ok || !consistent()) {
+      [parent, offset] = saved;
+      members.clear();
+      saved[2].forEach((id) => members.add(id));
+      elided.delete(k);
+    }
+  });
+
+  // groups start at their lowest member
+  const low = new Map(), high = new Map();
+  for (const id of members) {
+    const [r, d] = find(id);
+    low.set(r, Math.min(low.has(r) ? low.get(r) : d, d));
+    high.set(r, Math.max(high.has(r) ? high.get(r) : -Infinity, d + valueBytes(values[id])));
+  }
+  const place = new Map(), groupBytes = new Map();
+  for (const id of members) {
+    const [r, d] = find(id);
+    place.set(id, { root: r, off: d - low.get(r) });
+  }
+  for (const [r, lo] of low) groupBytes.set(r, high.get(r) - lo);
+  return { place, groupBytes, elided };
 }
 
 // ------------------------------------------------------------------ operators
@@ -517,5 +719,5 @@ function fromFloat16Array(bits) {
 module.exports = {
   GPUBufferUsage, MAX_NDIM, DTYPE_BYTESIZE, Tensor, WgpuExecutionContext, WgxDevice, WgxBuffer,
   requestDevice, createDevice, resolveArgs, shaders, shaderRegistry, toHalf, fromHalf,
-  toFloat16Array, fromFloat16Array,
+  toFloat16Array, fromFloat16Array, _planViews: planViews,
 };

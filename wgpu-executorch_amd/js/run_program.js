@@ -14,15 +14,15 @@
  *                    (HIP events on the queue)
  * and, with --out, writes the output tensor's bytes after the timed frames.
  * --record-only validates and records the program without running it (it
- * works on the host-only device -1).  --no-fuse records every op of the chain
- * as it stands (no conv -> sigmoid -> mul folding).
+ * works on the host-only device -1).  --no-fuse records no conv -> sigmoid ->
+ * mul folding, --no-views runs every cat / split / view_copy as a copy.
  */
 const fs = require('fs');
 const path = require('path');
 const W = require('./index.js');
 
 function parseArgs(argv) {
-  const a = { dir: null, device: 0, warmup: 5, reps: 50, out: null, recordOnly: false, fuse: true };
+  const a = { dir: null, device: 0, warmup: 5, reps: 50, out: null, recordOnly: false, fuse: true, views: true };
   for (let i = 0; i < argv.length; i++) {
     const k = argv[i];
     if (k === '--device') a.device = Number(argv[++i]);
@@ -31,6 +31,7 @@ function parseArgs(argv) {
     else if (k === '--out') a.out = argv[++i];
     else if (k === '--record-only') a.recordOnly = true;
     else if (k === '--no-fuse') a.fuse = false;
+    else if (k === '--no-views') a.views = false;
     else a.dir = k;
   }
   if (!a.dir) throw new Error('usage: node run_program.js DIR [--device N] [--warmup W] [--reps R] [--out FILE]');
@@ -53,7 +54,7 @@ async function main() {
   const output = ctx.tensor(outV.dtype, outV.shape);
 
   const t0 = process.hrtime.bigint();
-  ctx.recordProgram(program, weights, [input, output], { fuse: args.fuse });
+  ctx.recordProgram(program, weights, [input, output], { fuse: args.fuse, views: args.views });
   const recordMs = Number(process.hrtime.bigint() - t0) / 1e6;
   if (args.recordOnly) {
     console.log(JSON.stringify({ record_ms: recordMs, commands: ctx.commandCount, ops: program.chain.length }));
