@@ -104,7 +104,7 @@ def test_buffer_bounds_are_enforced(hctx, pkg):
         hctx.mm(big.__class__.__new__(W.Tensor) if False else big, t, t)
 
 
-def test_conv_validation_and_variants(hctx, pkg):
+def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     E = pkg.wgx.WgxError
     T = hctx.tensor
 
@@ -115,9 +115,18 @@ def test_conv_validation_and_variants(hctx, pkg):
         hctx.convolution(x, w, b, stride, pad, dil, transposed, op, groups, y)
         return hctx.last_kernel
 
-    assert "_conv" in conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1))
-    # 100 output tiles for 256 CUs: K = 1152 is split into ranges (suffix _k<ranges>)
+    # fewer 64 x 64 tiles than CUs: the wave-split kernel, 64 x 32 tiles with
+    # 4 waves (400 of them) or 8 waves (200)
+    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)) == "gemm_mfma_f16_64x32w4_conv_ws"
+    assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "gemm_mfma_f16_64x32w8_conv_ws"
+    assert conv([1, 64, 20, 20], [64, 64, 3, 3], [1, 64, 20, 20], pad=(1, 1), dtype="float32") == "gemm_mfma_f32_32x32w8_conv_ws"
+    assert conv([1, 64, 160, 160], [64, 64, 3, 3], [1, 64, 160, 160], pad=(1, 1)) == "gemm_mfma_f16_64x64w4_conv"
+    # without it, 100 output tiles for 256 CUs split K = 1152 into ranges (suffix _k<ranges>)
+    monkeypatch.setenv("WGX_WS", "off")
     assert "_conv_k" in conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1))
+    monkeypatch.setenv("WGX_WS", "1x2w4")
+    assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "gemm_mfma_f16_32x64w4_conv_ws"
+    monkeypatch.delenv("WGX_WS")
     assert "_kn" in conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8])
     assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3s1_r4v8"
     assert conv([1, 512, 20, 20], [512, 1, 5, 5], [1, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5s2_r4v4"

@@ -251,3 +251,34 @@ def test_conv_with_clamp_epilogue(gpu_ctx, orc, pkg, dtype):
                                out_shape=list(ref.shape), clamp=(0.0, 6.0))
         assert got.min() >= 0.0 and got.max() <= 6.0
         assert_parity(got, np.clip(ref, 0.0, 6.0), refa, dtype, ws[1] * 9, f"clamp {kernel}")
+
+
+WS_CONFIGS = ["1x1w4", "1x1w8", "2x1w4", "2x1w8", "1x2w4"]
+WS_CASES = [
+    # x shape, w shape, stride, pad, dilation: ragged M and N, batch 2,
+    # dilation, 5x5, a K range that is not a multiple of the 64-wide slice
+    ((1, 16, 21, 13), (24, 16, 3, 3), (1, 1), (1, 1), (1, 1)),
+    ((2, 24, 15, 15), (40, 24, 3, 3), (1, 1), (2, 2), (2, 2)),
+    ((1, 16, 33, 31), (72, 16, 5, 5), (2, 1), (2, 1), (1, 1)),
+    ((1, 64, 20, 20), (64, 64, 3, 3), (1, 1), (1, 1), (1, 1)),
+    ((1, 128, 10, 10), (100, 128, 3, 3), (2, 2), (1, 1), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("cfg", WS_CONFIGS)
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_wave_split_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg):
+    """Every instantiated wave-split configuration (forced through WGX_WS)
+    against the float64 convolution, including batch 2 and ragged tiles."""
+    monkeypatch.setenv("WGX_WS", cfg)
+    I = pkg.inputs
+    for i, (xs, ws, s, p, d) in enumerate(WS_CASES):
+        x = round_in(I.uniform(800 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(810 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(820 + i, (ws[0],), -0.5, 0.5), dtype) if i % 2 else None
+        ref, refa = orc.conv2d_f64(x, w, b, s, p, d, 1)
+        got, kernel = run_conv(gpu_ctx, x, w, b, dtype, s, p, d, 1, out_shape=list(ref.shape))
+        tm, tn = cfg.split("w")[0].split("x")
+        assert kernel.endswith(f"_{32 * int(tm)}x{32 * int(tn)}w{cfg.split('w')[1]}_conv_ws"), kernel
+        K = ws[1] * ws[2] * ws[3]
+        assert_parity(got, ref, refa, dtype, K, f"ws {cfg} case {i} {dtype} {xs}x{ws} {kernel}")

@@ -175,3 +175,25 @@ def test_large_tile_kernel_edges(gpu_ctx, orc, pkg, tile, monkeypatch):
     assert kernel.endswith("_nk_big"), kernel
     ref, refa = orc.gemm_f64(A, B)
     assert_parity(to.get_f32(), ref, refa, "float16", 72, f"big bmm {tile} {kernel}")
+
+
+@pytest.mark.parametrize("cfg", ["1x1w4", "1x1w8", "2x1w4", "2x1w8", "1x2w4"])
+def test_wave_split_f32_gemm(gpu_ctx, orc, pkg, monkeypatch, cfg):
+    """fp32 GEMMs with few tiles on every wave-split configuration: both B
+    layouts (the same bits either way), ragged edges, alpha / beta / bias."""
+    monkeypatch.setenv("WGX_WS", cfg)
+    I = pkg.inputs
+    for i, (M, K, N) in enumerate([(512, 512, 512), (100, 72, 130), (33, 256, 65)]):
+        A = I.uniform(900 + i, (M, K), -1, 1).astype(np.float32)
+        B = I.uniform(910 + i, (K, N), -1, 1).astype(np.float32)
+        bias = I.uniform(920 + i, (N,), -0.5, 0.5).astype(np.float32)
+        alpha, beta = (1.0, 1.0) if i == 0 else (0.75, -1.5)
+        nn, k_nn = run_mm(gpu_ctx, A, B, "float32", bias=bias, alpha=alpha, beta=beta)
+        nt, k_nt = run_mm(gpu_ctx, A, np.ascontiguousarray(B.T), "float32", bias=bias, alpha=alpha,
+                          beta=beta, trans_b=True)
+        assert k_nn.endswith("_kn_ws") and k_nt.endswith("_nk_ws"), (k_nn, k_nt)
+        ref, refa = orc.gemm_f64(A, B, None)
+        ref = alpha * ref + beta * bias.astype(np.float64)
+        refa = abs(alpha) * refa + abs(beta) * np.abs(bias.astype(np.float64))
+        assert_parity(nn, ref, refa, "float32", K, f"ws {cfg} mm {M}x{K}x{N} {k_nn}")
+        assert np.array_equal(nn.view(np.uint32), nt.view(np.uint32)), f"ws {cfg} {M}x{K}x{N}: NN != NT"

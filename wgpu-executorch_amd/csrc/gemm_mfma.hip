@@ -35,6 +35,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <type_traits>
 
@@ -1392,6 +1393,256 @@ hipError_t launch_nk(const KParams& kp, int batch, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ============================================================ wave-split kernel
+// GEMMs with few output tiles -- convolutions as implicit im2col (B_CONV)
+// or 1x1 (B_KN, the input plane as a [K, N] operand), small mm / addmm in
+// either weight layout (B_KN, B_NK): a 20x20 to 80x80 map at
+// batch 1 gives 25 to 400 tiles of 32 x 32 for 256 CUs, and a block of the
+// tiled kernels above then waits out about one memory latency per K slice,
+// its K slices one after another.  Here the W waves of a block share ONE
+// output tile of (TM*32) x (TN*32) and split its K slices among themselves
+// (wave w takes slices w, w+W, w+2W, ...).  Each wave loads its MFMA
+// fragments from global memory straight into registers -- A rows as 16-byte
+// chunks, B as 16-byte chunks of [N, K] rows or as element gathers (im2col
+// taps through the per-launch tap table, kept in LDS, or n-strided rows);
+// both layouts give every lane the same k run, so an mm gives the same bits
+// with either weight layout -- with the next slice's loads in
+// flight during the current slice's MFMAs; the K loop has no barrier.  After it every wave parks its partial
+// sums in LDS and each wave finishes a share of the tile's register groups:
+// the W partials are added in wave order (fixed, so the result does not
+// depend on timing), then bias, activation, clamp and one rounding.
+template <int DT, int BMODE, int TM, int TN, int W>
+__global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
+  constexpr int ES = DT == DT_F32 ? 4 : 2;
+  constexpr int EPC = 16 / ES;     // elements per 16-byte chunk
+  constexpr int BK = 128 / ES;     // k per slice
+  constexpr int NG = TM * TN * 4;  // accumulator groups of 4 per lane
+  constexpr int BM = TM * 32, BN = TN * 32;
+  constexpr bool CONV = BMODE == B_CONV;
+  constexpr bool NK = BMODE == B_NK;
+  extern __shared__ uint4 ws_lds[];  // tap table (B_CONV), then partials [W][NG][64] float4
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = p.M, N = p.N, K = p.K;
+  const int KT = (K + BK - 1) / BK;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_mn = tiles_m * p.tiles_n;
+  // XCD-aware numbering; m-tiles vary fastest, so the blocks of one XCD
+  // share the B columns (the gathered operand) in its L2
+  const int G = gridDim.x;
+  const int rb = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int z = rb / tiles_mn, rt = rb - z * tiles_mn;
+  const int m0 = (rt % tiles_m) * BM, n0 = (rt / tiles_m) * BN;
+
+  const uint32_t* ktab = reinterpret_cast<const uint32_t*>(ws_lds);
+  float4* part = reinterpret_cast<float4*>(ws_lds + (CONV ? KT * BK / 4 : 0));
+
+  const int fr = lane & 31, fc = lane >> 5;
+  const int mrows = min(BM, M - m0);
+  const rsrc_t ra = make_rsrc(reinterpret_cast<const char*>(p.A) + ((long long)z * p.sA + (long long)m0 * p.lda) * ES,
+                              (uint32_t)((mrows - 1) * p.lda + K) * ES);
+  // B_CONV: one input image; B_KN / B_NK: the [K, ldb] / [N, ldb] matrix
+  // (ranges checked by the host)
+  const rsrc_t rbs = make_rsrc(reinterpret_cast<const char*>(p.B) + (long long)z * p.sB * ES,
+                               CONV ? p.b_bytes
+                               : NK ? (uint32_t)((long long)(N - 1) * p.ldb + K) * ES
+                                    : (uint32_t)((long long)(K - 1) * p.ldb + N) * ES);
+  uint32_t aoff[TM];
+  bool aok[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    aok[i] = i * 32 + fr < mrows;
+    aoff[i] = (uint32_t)((i * 32 + fr) * p.lda) * ES;
+  }
+  // per column: base offset of the output pixel's window and the mask of the
+  // kernel taps that land inside the image (zero past N: every load reads 0)
+  int colbase[TN];
+  unsigned long long cmask[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + j * 32 + fr;
+    colbase[j] = 0;
+    cmask[j] = 0ull;
+    if (!CONV) {
+      colbase[j] = col;
+      cmask[j] = col < N ? ~0ull : 0ull;
+    } else if (col < N) {
+      const ConvGeom& g = p.g;
+      const int oh = col / g.OW, ow = col - oh * g.OW;
+      const int ih0 = oh * g.sH - g.pH, iw0 = ow * g.sW - g.pW;
+      colbase[j] = ih0 * g.IW + iw0;
+      for (int kh = 0; kh < g.KH; ++kh) {
+        const int ih = ih0 + kh * g.dH;
+        if (ih < 0 || ih >= g.IH) continue;
+        for (int kw = 0; kw < g.KW; ++kw) {
+          const int iw = iw0 + kw * g.dW;
+          if (iw >= 0 && iw < g.IW) cmask[j] |= 1ull << (kh * g.KW + kw);
+        }
+      }
+    }
+  }
+  struct Frag {
+    uint4 a[TM][4];
+    uint32_t b[TN][4][NK ? 1 : EPC];  // gathered elements
+    uint4 bv[TN][NK ? 4 : 1];         // [N, K] rows: one chunk per k-step
+  };
+  // slice s: per k-step kk (16 bytes of k per lane), the lane's chunk kk*2+fc
+  auto loadA = [&](Frag& F, int s) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int kc = s * BK + (kk * 2 + fc) * EPC;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) F.a[i][kk] = ld_b128(ra, (aok[i] && kc < K) ? aoff[i] + (uint32_t)kc * ES : OOB);
+    }
+  };
+  auto loadB = [&](Frag& F, int s) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int kc = s * BK + (kk * 2 + fc) * EPC;
+      if constexpr (CONV) {
+        uint32_t ent[EPC];
+#pragma unroll
+        for (int q = 0; q < EPC; q += 4) {
+          const uint4 e4 = *reinterpret_cast<const uint4*>(ktab + kc + q);
+          ent[q] = e4.x;
+          ent[q + 1] = e4.y;
+          ent[q + 2] = e4.z;
+          ent[q + 3] = e4.w;
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) {
+            const bool ok = (cmask[j] >> (ent[e] & 63u)) & 1ull;
+            const uint32_t off = ok ? (uint32_t)(colbase[j] + (int)(ent[e] >> 6)) * ES : OOB;
+            F.b[j][kk][e] = ES == 4 ? ld_b32(rbs, off) : ld_b16(rbs, off);
+          }
+      } else if constexpr (NK) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          F.bv[j][kk] = ld_b128(rbs, (cmask[j] && kc < K) ? (uint32_t)(colbase[j] * p.ldb + kc) * ES : OOB);
+      } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) {
+            const uint32_t off = (cmask[j] && kc + e < K) ? (uint32_t)((kc + e) * p.ldb + colbase[j]) * ES : OOB;
+            F.b[j][kk][e] = ES == 4 ? ld_b32(rbs, off) : ld_b16(rbs, off);
+          }
+      }
+    }
+  };
+  auto load = [&](Frag& F, int s) {
+    loadA(F, s);
+    loadB(F, s);
+  };
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  auto mma = [&](const Frag& F) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        uint4 bq;
+        if constexpr (NK)
+          bq = F.bv[j][kk];
+        else if constexpr (ES == 4)
+          bq = make_uint4(F.b[j][kk][0], F.b[j][kk][1], F.b[j][kk][2], F.b[j][kk][3]);
+        else
+          bq = make_uint4(pack2(F.b[j][kk][0], F.b[j][kk][1]), pack2(F.b[j][kk][2], F.b[j][kk][3]),
+                          pack2(F.b[j][kk][4], F.b[j][kk][5]), pack2(F.b[j][kk][6], F.b[j][kk][7]));
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i][j] = mfma_frag<DT>(bq, F.a[i][kk], acc[i][j]);
+      }
+  };
+
+  // two register sets: the loads of slice s+W fly while slice s is multiplied
+  // The first slice's A loads go out before the tap table is staged in LDS.
+  Frag F0, F1;
+  int s = wave;
+  if (s < KT) loadA(F0, s);
+  if constexpr (CONV) {
+    for (int i = tid; i < KT * BK / 4; i += W * 64) ws_lds[i] = reinterpret_cast<const uint4*>(p.ktab)[i];
+    __syncthreads();
+  }
+  if (s < KT) loadB(F0, s);
+  while (s < KT) {
+    if (s + W < KT) load(F1, s + W);
+    mma(F0);
+    s += W;
+    if (s >= KT) break;
+    if (s + W < KT) load(F0, s + W);
+    mma(F1);
+    s += W;
+  }
+
+  // partial sums -> LDS, then each wave reduces groups wave, wave+W, ...
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        part[(wave * NG + (i * TN + j) * 4 + g) * 64 + lane] =
+            make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+  __syncthreads();
+
+  const rsrc_t rc = make_rsrc(reinterpret_cast<char*>(p.C) + ((long long)z * p.sC + (long long)m0 * p.ldc + n0) * ES,
+                              (uint32_t)((mrows - 1) * p.ldc + (N - n0)) * ES);
+  const bool cvec = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & (4 * ES - 1)) == 0) &&
+                    ((p.sC & 3) == 0) && ((N & 3) == 0);
+  auto bias_at = [&](int idx) -> float {
+    if constexpr (DT == DT_F32) return reinterpret_cast<const float*>(p.bias)[idx];
+    else return to_f32<DT>(p.bias[idx]);
+  };
+  for (int q = wave; q < NG; q += W) {
+    float4 v = part[q * 64 + lane];
+    for (int w = 1; w < W; ++w) {
+      const float4 t = part[(w * NG + q) * 64 + lane];
+      v.x += t.x;
+      v.y += t.y;
+      v.z += t.z;
+      v.w += t.w;
+    }
+    const int i = q / (TN * 4), j = (q >> 2) % TN, g = q & 3;
+    const int row = i * 32 + fr;
+    const int col = j * 32 + 8 * g + 4 * fc;
+    if (row >= mrows) continue;
+    const float rowb = p.bias_mode == BIAS_ROW ? p.beta * bias_at(m0 + row) : 0.0f;
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = p.alpha * vv[e] + rowb;
+      if (p.bias_mode == BIAS_COL && n0 + col + e < N) x += p.beta * bias_at(n0 + col + e);
+      x = apply_act(p.act, x);
+      if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+      if constexpr (DT == DT_F32) h[e] = __float_as_uint(x);
+      else h[e] = st_bits<DT == DT_BF16>(x);
+    }
+    const uint32_t off = (uint32_t)(row * p.ldc + col) * ES;
+    if (cvec) {
+      if constexpr (DT == DT_F32)
+        st_b128(make_uint4(h[0], h[1], h[2], h[3]), rc, n0 + col < N ? off : OOB);
+      else
+        st_b64(make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3])), rc, n0 + col < N ? off : OOB);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t oe = n0 + col + e < N ? off + ES * e : OOB;
+        if constexpr (DT == DT_F32) st_b32(h[e], rc, oe);
+        else st_b16(h[e], rc, oe);
+      }
+    }
+  }
+}
+
 // Split-K reduction: C = epilogue(sum over ranges of ws[r]), the ranges
 // summed in order 0..splits-1 so the result does not depend on scheduling.
 // One thread per 4 consecutive outputs of a row.
@@ -1541,6 +1792,46 @@ hipError_t launch_one3(const KParams& kp, int batch, hipStream_t s) {
   }
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WGM * WGN * 64), dyn, s, k2);
   return hipGetLastError();
+}
+
+// Wave-split kernel configurations: wave tile (TM*32) x (TN*32), W waves.
+struct WsCfg {
+  int tm, tn, w;
+};
+constexpr WsCfg kWsCfgs[] = {{1, 1, 4}, {1, 1, 8}, {2, 1, 4}, {2, 1, 8}, {1, 2, 4}};
+
+template <int DT, int BMODE, int TM, int TN, int W>
+hipError_t launch_ws(const KParams& kp, int batch, hipStream_t s) {
+  auto fn = k_gemm_ws<DT, BMODE, TM, TN, W>;
+  constexpr int BK = DT == DT_F32 ? 32 : 64;
+  const int kt = (kp.K + BK - 1) / BK;
+  const size_t dyn = (BMODE == B_CONV ? (size_t)kt * BK * 4 : 0) + (size_t)W * TM * TN * 4 * 64 * 16;
+  if (dyn > 160 * 1024) return hipErrorInvalidValue;
+  static size_t attr_dyn = 0;  // largest dynamic size allowed so far
+  if (dyn > attr_dyn && s != name_only()) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
+    if (e != hipSuccess) return e;
+    attr_dyn = dyn;
+  }
+  if (is_dry(s)) return hipSuccess;
+  KParams k2 = kp;
+  k2.batch = batch;
+  k2.tiles_n = (kp.N + TN * 32 - 1) / (TN * 32);
+  const long long grid = (long long)((kp.M + TM * 32 - 1) / (TM * 32)) * k2.tiles_n * batch;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(W * 64), dyn, s, k2);
+  return hipGetLastError();
+}
+
+template <int DT, int BMODE>
+hipError_t dispatch_ws(const WsCfg& c, const KParams& kp, int batch, hipStream_t s) {
+  if (c.tm == 1 && c.tn == 1 && c.w == 4) return launch_ws<DT, BMODE, 1, 1, 4>(kp, batch, s);
+  if (c.tm == 1 && c.tn == 1 && c.w == 8) return launch_ws<DT, BMODE, 1, 1, 8>(kp, batch, s);
+  if (c.tm == 2 && c.tn == 1 && c.w == 4) return launch_ws<DT, BMODE, 2, 1, 4>(kp, batch, s);
+  if (c.tm == 2 && c.tn == 1 && c.w == 8) return launch_ws<DT, BMODE, 2, 1, 8>(kp, batch, s);
+  if (c.tm == 1 && c.tn == 2 && c.w == 4) return launch_ws<DT, BMODE, 1, 2, 4>(kp, batch, s);
+  return hipErrorNotSupported;
 }
 
 struct Tile {
@@ -1704,6 +1995,50 @@ Plan make_plan(const GemmDesc& d) {
   return pl;
 }
 
+// Whether a launch runs the wave-split kernel, and with which configuration:
+// convolutions (implicit im2col, fp32 / fp16) and fp32 GEMMs of either B
+// layout whose 64 x 64 tiles number fewer than the CUs.  (An fp16 [K, N]
+// operand loses here: its 2-byte gathers at stride N are slower than the
+// tiled kernel's 16-byte row loads with an in-register transpose; [N, K]
+// stays with it too, so an mm gives the same bits in either layout.)  The
+// configuration aims at 1000-2000 waves: measured on MI355X over the 3x3
+// and 1x1 convolutions of 20x20 to 80x80 maps, 32 x 32 tiles with 8 waves
+// win up to one tile per CU, 64 x 32 tiles above that.  WGX_WS="off"
+// disables the kernel, "TMxTNwW" forces a configuration wherever it applies.
+bool ws_choice(const GemmDesc& d, const Plan& pl, WsCfg* cfg) {
+  if (!pl.avec || pl.bf) return false;
+  if (d.bmode == B_CONV) {
+    if (!d.ktab) return false;
+  } else if (!pl.f32) {
+    return false;
+  } else if (d.bmode == B_KN) {
+    // the [K, ldb] plane is one buffer range with 32-bit offsets
+    if (((long long)(d.K - 1) * d.ldb + d.N) * pl.es >= (1LL << 31)) return false;
+  } else {
+    if (!pl.bvec || ((long long)(d.N - 1) * d.ldb + d.K) * pl.es >= (1LL << 31)) return false;
+  }
+  const char* force = getenv("WGX_WS");
+  if (force) {
+    if (strcmp(force, "off") == 0) return false;
+    int tm = 0, tn = 0, w = 0;
+    if (sscanf(force, "%dx%dw%d", &tm, &tn, &w) == 3)
+      for (const WsCfg& c : kWsCfgs)
+        if (c.tm == tm && c.tn == tn && c.w == w) {
+          *cfg = c;
+          return true;
+        }
+  }
+  const long long cus = device_cus();
+  const long long tiles64 = (long long)((d.M + 63) / 64) * ((d.N + 63) / 64) * d.batch;
+  if (tiles64 >= cus) return false;
+  const long long tiles32 = (long long)((d.M + 31) / 32) * ((d.N + 31) / 32) * d.batch;
+  const long long tiles2 = (long long)((d.M + 63) / 64) * ((d.N + 31) / 32) * d.batch;
+  if (tiles32 <= cus) *cfg = WsCfg{1, 1, 8};
+  else if (pl.f32) *cfg = WsCfg{2, 1, 4};
+  else *cfg = tiles2 <= cus ? WsCfg{2, 1, 8} : WsCfg{2, 1, 4};
+  return true;
+}
+
 }  // namespace
 
 // Split K when the tiles alone leave CUs idle: the number of ranges that
@@ -1713,7 +2048,8 @@ Plan make_plan(const GemmDesc& d) {
 int gemm_split_plan(const GemmDesc& d, size_t* ws_bytes) {
   *ws_bytes = 0;
   const Plan pl = make_plan(d);
-  if (!pl.pipelined || pl.big) return 1;
+  WsCfg wc;
+  if (!pl.pipelined || pl.big || ws_choice(d, pl, &wc)) return 1;
   const long long ntiles =
       (long long)((d.M + pl.t.bm - 1) / pl.t.bm) * ((d.N + pl.t.bn - 1) / pl.t.bn) * d.batch;
   const int kt = (d.K + 128 / pl.es - 1) / (128 / pl.es);
@@ -1799,6 +2135,21 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
     if (b.bm == 256 && b.bn == 128)
       return bf ? launch_nk<256, 128, 2, 2, true, 3, 128>(kp, d.batch, s) : launch_nk<256, 128, 2, 2, false, 3, 128>(kp, d.batch, s);
     return bf ? launch_nk<192, 256, 2, 2, true, 5, 64>(kp, d.batch, s) : launch_nk<192, 256, 2, 2, false, 5, 64>(kp, d.batch, s);
+  }
+  WsCfg wc;
+  if (d.splits <= 1 && ws_choice(d, pl, &wc)) {
+    if (name) {
+      char buf[96];
+      snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw%d_%s_ws", f32 ? "f32" : "f16", 32 * wc.tm, 32 * wc.tn, wc.w,
+               d.bmode == B_CONV ? "conv" : (d.bmode == B_NK ? "nk" : "kn"));
+      *name = buf;
+    }
+    kp.tiles_n = (d.N + 32 * wc.tn - 1) / (32 * wc.tn);
+    if (d.bmode == B_CONV)
+      return f32 ? dispatch_ws<DT_F32, B_CONV>(wc, kp, d.batch, s) : dispatch_ws<DT_F16, B_CONV>(wc, kp, d.batch, s);
+    if (d.bmode == B_NK)
+      return f32 ? dispatch_ws<DT_F32, B_NK>(wc, kp, d.batch, s) : dispatch_ws<DT_F16, B_NK>(wc, kp, d.batch, s);
+    return f32 ? dispatch_ws<DT_F32, B_KN>(wc, kp, d.batch, s) : dispatch_ws<DT_F16, B_KN>(wc, kp, d.batch, s);
   }
   const bool knv = d.bmode == B_KN && bvec;
   if (name) {
