@@ -1457,6 +1457,15 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
   }
   // per column: base offset of the output pixel's window and the mask of the
   // kernel taps that land inside the image (zero past N: every load reads 0)
+  auto bias_at = [&](int idx) -> float {
+    if constexpr (DT == DT_F32) return reinterpret_cast<const float*>(p.bias)[idx];
+    else return to_f32<DT>(p.bias[idx]);
+  };
+  // the lane's per-row bias, fetched now: off the epilogue's critical path
+  float brow[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+    brow[i] = (p.bias_mode == BIAS_ROW && i * 32 + fr < mrows) ? p.beta * bias_at(m0 + i * 32 + fr) : 0.0f;
   int colbase[TN];
   unsigned long long cmask[TN];
 #pragma unroll
@@ -1510,12 +1519,17 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
           ent[q + 2] = e4.z;
           ent[q + 3] = e4.w;
         }
+        // at most 31 taps (checked by the host; the table's padding entries,
+        // tap 63, then read bit 31, never set): v_bfe_u32 reads the tap's
+        // bit straight from the entry's low 5 bits, and a tap outside the
+        // image sets bit 31 of the offset (out of range: reads 0) -- no
+        // compare and select per element
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
           for (int e = 0; e < EPC; ++e) {
-            const bool ok = (cmask[j] >> (ent[e] & 63u)) & 1ull;
-            const uint32_t off = ok ? (uint32_t)(colbase[j] + (int)(ent[e] >> 6)) * ES : OOB;
+            const uint32_t ok = __builtin_amdgcn_ubfe((uint32_t)cmask[j], ent[e], 1u);
+            const uint32_t off = ((uint32_t)(colbase[j] + (int)(ent[e] >> 6)) * ES) | ((ok ^ 1u) << 31);
             F.b[j][kk][e] = ES == 4 ? ld_b32(rbs, off) : ld_b16(rbs, off);
           }
       } else if constexpr (NK) {
@@ -1564,6 +1578,12 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
 
   // two register sets: the loads of slice s+W fly while slice s is multiplied
   // The first slice's A loads go out before the tap table is staged in LDS.
+  // (Measured on MI355X: this plain form beats an unconditional prefetch
+  // and a schedule pinned with sched_barrier.  A slice is bound by the VALU
+  // work of the gather addresses -- tap mask, offset, select: about 6
+  // instructions per element, some 250 per slice against 128 MFMA cycles --
+  // and 36 loads per slice in flight twice would pass the 63 that vmcnt
+  // tracks.)
   Frag F0, F1;
   int s = wave;
   if (s < KT) loadA(F0, s);
@@ -1597,10 +1617,6 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
                               (uint32_t)((mrows - 1) * p.ldc + (N - n0)) * ES);
   const bool cvec = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & (4 * ES - 1)) == 0) &&
                     ((p.sC & 3) == 0) && ((N & 3) == 0);
-  auto bias_at = [&](int idx) -> float {
-    if constexpr (DT == DT_F32) return reinterpret_cast<const float*>(p.bias)[idx];
-    else return to_f32<DT>(p.bias[idx]);
-  };
   for (int q = wave; q < NG; q += W) {
     float4 v = part[q * 64 + lane];
     for (int w = 1; w < W; ++w) {
@@ -1614,7 +1630,10 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
     const int row = i * 32 + fr;
     const int col = j * 32 + 8 * g + 4 * fc;
     if (row >= mrows) continue;
-    const float rowb = p.bias_mode == BIAS_ROW ? p.beta * bias_at(m0 + row) : 0.0f;
+    float rowb = 0.0f;
+#pragma unroll
+    for (int ii = 0; ii < TM; ++ii)
+      if (ii == i) rowb = brow[ii];
     const float vv[4] = {v.x, v.y, v.z, v.w};
     uint32_t h[4];
 #pragma unroll
@@ -2008,7 +2027,7 @@ Plan make_plan(const GemmDesc& d) {
 bool ws_choice(const GemmDesc& d, const Plan& pl, WsCfg* cfg) {
   if (!pl.avec || pl.bf) return false;
   if (d.bmode == B_CONV) {
-    if (!d.ktab) return false;
+    if (!d.ktab || d.g.KH * d.g.KW > 31) return false;  // bit 31: the table's padding tap
   } else if (!pl.f32) {
     return false;
   } else if (d.bmode == B_KN) {

@@ -15,14 +15,16 @@
  * and, with --out, writes the output tensor's bytes after the timed frames.
  * --record-only validates and records the program without running it (it
  * works on the host-only device -1).  --no-fuse records no conv -> sigmoid ->
- * mul folding, --no-views runs every cat / split / view_copy as a copy.
+ * mul folding, --no-views runs every cat / split / view_copy as a copy,
+ * --eager replays the recorded launches one by one on the stream instead of
+ * through a HIP graph.
  */
 const fs = require('fs');
 const path = require('path');
 const W = require('./index.js');
 
 function parseArgs(argv) {
-  const a = { dir: null, device: 0, warmup: 5, reps: 50, out: null, recordOnly: false, fuse: true, views: true };
+  const a = { dir: null, device: 0, warmup: 5, reps: 50, out: null, recordOnly: false, fuse: true, views: true, eager: false };
   for (let i = 0; i < argv.length; i++) {
     const k = argv[i];
     if (k === '--device') a.device = Number(argv[++i]);
@@ -32,6 +34,7 @@ function parseArgs(argv) {
     else if (k === '--record-only') a.recordOnly = true;
     else if (k === '--no-fuse') a.fuse = false;
     else if (k === '--no-views') a.views = false;
+    else if (k === '--eager') a.eager = true;
     else a.dir = k;
   }
   if (!a.dir) throw new Error('usage: node run_program.js DIR [--device N] [--warmup W] [--reps R] [--out FILE]');
@@ -53,6 +56,7 @@ async function main() {
   input.setData(new Uint8Array(ibuf.buffer, ibuf.byteOffset, ibuf.byteLength));
   const output = ctx.tensor(outV.dtype, outV.shape);
 
+  if (args.eager) ctx.setGraphMode(false);
   const t0 = process.hrtime.bigint();
   ctx.recordProgram(program, weights, [input, output], { fuse: args.fuse, views: args.views });
   const recordMs = Number(process.hrtime.bigint() - t0) / 1e6;
