@@ -168,6 +168,18 @@ int wgx_record_bmm(wgx_ctx* ctx, const wgx_tensor* a, const wgx_tensor* b,
 int wgx_record_conv2d(wgx_ctx* ctx, const wgx_tensor* in, const wgx_tensor* weight,
                       const wgx_tensor* bias, const wgx_conv_args* args,
                       const wgx_tensor* out);
+/* The same convolution with an output-shaped tensor added in its epilogue:
+ * out = conv_scale * conv(in) + residual_scale * residual, where conv(in) is
+ * the full result above (bias, activation, clamp), rounded once.  No
+ * counterpart in the reference: recordProgram folds
+ * aten.add.Tensor(a, b, alpha) into the convolution that produces a or b
+ * with it (src/shaders/add/index.ts:33-129: out = a + alpha * b).  Depthwise
+ * convolutions only; residual may be the output itself but must not
+ * partly overlap it. */
+int wgx_record_conv2d_residual(wgx_ctx* ctx, const wgx_tensor* in, const wgx_tensor* weight,
+                               const wgx_tensor* bias, const wgx_conv_args* args,
+                               const wgx_tensor* residual, float conv_scale,
+                               float residual_scale, const wgx_tensor* out);
 
 /* Elementwise / data-movement ops a YOLO-style program chain needs (simple,
  * bandwidth-bound kernels; not the optimisation target). */

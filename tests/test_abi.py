@@ -182,3 +182,27 @@ def test_im2col_table_matches_oracle_indexing(pkg, orc):
                 cols[k, n] = x.ravel()[ih0 * IW + iw0 + off]
     got = w.reshape(4, K).astype(np.float64) @ cols
     assert np.max(np.abs(got - y.reshape(4, -1))) < 1e-12
+
+
+def test_conv_residual_validation(hctx, pkg):
+    """The residual epilogue's checks: depthwise only, the output's shape and
+    dtype, the output itself or no overlap at all."""
+    E = pkg.wgx.WgxError
+    T = hctx.tensor
+    x, w, b = T("float16", [1, 8, 10, 10]), T("float16", [8, 1, 3, 3]), T("float16", [8])
+    y, r = T("float16", [1, 8, 10, 10]), T("float16", [1, 8, 10, 10])
+    hctx.convolution(x, w, b, 1, 1, 1, False, 0, 8, y, residual=r, residual_scale=0.5)
+    assert hctx.last_kernel.startswith("depthwise_f16_3x3s1")
+    hctx.convolution(x, w, b, 1, 1, 1, False, 0, 8, y, residual=y)  # in place
+    with pytest.raises(E, match="depthwise convolutions only"):
+        hctx.convolution(x, T("float16", [8, 8, 3, 3]), b, 1, 1, 1, False, 0, 1, y, residual=r)
+    with pytest.raises(E, match="match the output"):
+        hctx.convolution(x, w, b, 1, 1, 1, False, 0, 8, y, residual=T("float16", [1, 8, 10, 11]))
+    with pytest.raises(E, match="match the output"):
+        hctx.convolution(x, w, b, 1, 1, 1, False, 0, 8, y, residual=T("float32", [1, 8, 10, 10]))
+    buf = hctx.storage_buffer(2 * 800 + 64)
+    W = pkg.wgx
+    y2 = W.Tensor(hctx, "float16", [1, 8, 10, 10], buf, 2 * 800 + 64)
+    r2 = W.Tensor(hctx, "float16", [1, 8, 10, 10], buf + 32, 2 * 800 + 32)
+    with pytest.raises(E, match="partly overlaps"):
+        hctx.convolution(x, w, b, 1, 1, 1, False, 0, 8, y2, residual=r2)

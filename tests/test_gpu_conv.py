@@ -282,3 +282,40 @@ def test_wave_split_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg):
         assert kernel.endswith(f"_{32 * int(tm)}x{32 * int(tn)}w{cfg.split('w')[1]}_conv_ws"), kernel
         K = ws[1] * ws[2] * ws[3]
         assert_parity(got, ref, refa, dtype, K, f"ws {cfg} case {i} {dtype} {xs}x{ws} {kernel}")
+
+
+RESIDUAL_CASES = [
+    # x shape, w shape, stride, pad, dilation, (conv scale, residual scale), in place
+    ((1, 24, 16, 16), (24, 1, 3, 3), (1, 1), (1, 1), (1, 1), (1.0, 1.0), False),   # register kernel (fp16)
+    ((2, 16, 20, 20), (16, 1, 5, 5), (2, 2), (2, 2), (1, 1), (0.5, 1.0), False),   # register kernel, stride 2
+    ((1, 6, 13, 17), (6, 1, 3, 3), (1, 1), (1, 1), (1, 1), (1.0, -2.0), False),    # LDS kernel (odd width)
+    ((1, 8, 12, 12), (8, 1, 3, 3), (1, 1), (2, 2), (2, 2), (1.0, 1.0), False),     # generic (dilation 2)
+    ((1, 32, 10, 10), (32, 1, 3, 3), (1, 1), (1, 1), (1, 1), (1.0, 1.0), True),    # residual is the output
+]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_depthwise_silu_residual_epilogue(gpu_ctx, orc, pkg, dtype):
+    """Depthwise convolution + SiLU + an output-shaped residual in one launch,
+    out = cs * silu(conv) + rs * residual, against the fp64 oracle."""
+    W, I = pkg.wgx, pkg.inputs
+    for i, (xs, ws, s, p, d, (cs, rs), inplace) in enumerate(RESIDUAL_CASES):
+        g = xs[1]
+        x = round_in(I.uniform(1900 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(1910 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(1920 + i, (ws[0],), -0.5, 0.5), dtype)
+        ref, refa = orc.conv2d_f64(x, w, b, s, p, d, g)
+        r = round_in(I.uniform(1930 + i, ref.shape, -2, 2), dtype)
+        tx, tw, tb = gpu_ctx.from_numpy(x, dtype), gpu_ctx.from_numpy(w, dtype), gpu_ctx.from_numpy(b, dtype)
+        tr = gpu_ctx.from_numpy(r, dtype)
+        ty = tr if inplace else gpu_ctx.tensor(dtype, list(ref.shape))
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, tb, list(s), list(p), list(d), False, [0, 0], g, ty,
+                            activation=W.ACT_SILU, residual=tr, conv_scale=cs, residual_scale=rs)
+        kernel = gpu_ctx.last_kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        want = cs * (ref / (1.0 + np.exp(-ref))) + rs * r.astype(np.float64)
+        bound = 1.1 * abs(cs) * refa + abs(rs) * np.abs(r.astype(np.float64))
+        assert_parity(ty.get_f32(), want, bound, dtype, ws[1] * ws[2] * ws[3],
+                      f"residual {i} {dtype} {xs}x{ws} {kernel}")

@@ -96,7 +96,9 @@ def test_generator_pool_plan_follows_converter_rule(Y):
 def _expected_silu_fusions(prog):
     """conv -> sigmoid -> mul triples recordProgram folds: the two
     intermediates read by nothing else (a product that shares memory with the
-    convolution's input is moved, not left unfused)."""
+    convolution's input is moved, not left unfused).  Returns (triples, adds):
+    adds counts the triples whose next op is an add of the product (read by
+    nothing else) on a depthwise convolution, which join the launch too."""
     vals, chain = prog["values"], prog["chain"]
     uses = {}
     for op in chain:
@@ -105,7 +107,7 @@ def _expected_silu_fusions(prog):
                 uses[t] = uses.get(t, 0) + 1
     for t in prog["outputIds"]:
         uses[t] = uses.get(t, 0) + 1
-    n, k = 0, 0
+    n, adds, k = 0, 0, 0
     while k + 2 < len(chain):
         conv, sig, mul = chain[k:k + 3]
         c = conv["args"][-1]
@@ -114,12 +116,21 @@ def _expected_silu_fusions(prog):
         if ok:
             s = sig["args"][1]
             ok = sorted(mul["args"][:2]) == sorted([c, s]) and uses.get(c) == 3 and uses.get(s) == 2
-        if ok:
-            n += 1
-            k += 3
-        else:
+        if not ok:
             k += 1
-    return n
+            continue
+        n += 1
+        y, w = mul["args"][2], vals[conv["args"][1]]["shape"]
+        groups = vals[conv["args"][8]]["value"]
+        nxt = chain[k + 3] if k + 3 < len(chain) else None
+        if (nxt is not None and nxt["name"] == "aten.add.Tensor" and uses.get(y) == 2
+                and (nxt["args"][0] == y) != (nxt["args"][1] == y)
+                and w[1] == 1 and w[0] == groups == vals[conv["args"][0]]["shape"][1]):
+            adds += 1
+            k += 4
+        else:
+            k += 3
+    return n, adds
 
 
 def _expected_view_copies(prog):
@@ -157,13 +168,14 @@ def test_js_host_records_the_program(Y, tmp_path):
         assert res[flags]["ops"] == len(prog["chain"])
     base = res[("--no-fuse", "--no-views")]["commands"]
     assert base >= len(prog["chain"])
-    # every conv -> sigmoid -> mul the rule allows is one launch instead of three
-    n = _expected_silu_fusions(prog)
+    # every conv -> sigmoid -> mul the rule allows is one launch instead of
+    # three, and a residual add after a depthwise one joins it
+    n, adds = _expected_silu_fusions(prog)
     v = _expected_view_copies(prog)
-    assert n > 0 and v > 0
-    assert base - res[("--no-views",)]["commands"] == 2 * n
+    assert n > 0 and adds > 0 and v > 0
+    assert base - res[("--no-views",)]["commands"] == 2 * n + adds
     assert base - res[("--no-fuse",)]["commands"] == v
-    assert base - res[()]["commands"] == 2 * n + v
+    assert base - res[()]["commands"] == 2 * n + adds + v
 
 
 # ------------------------------------------------------------ evaluator pins

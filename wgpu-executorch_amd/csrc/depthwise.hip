@@ -60,6 +60,8 @@ struct DwParams {
   int has_clamp;
   int act;
   float cmin, cmax;
+  const void* res;  // residual (output-shaped) or null: y = rcs * y + rrs * res
+  float rcs, rrs;
 };
 
 template <int DT>
@@ -152,7 +154,9 @@ __global__ __launch_bounds__(NT) void k_depthwise(DwParams p) {
     }
     acc = apply_act(p.act, acc);
     if (p.has_clamp) acc = fminf(fmaxf(acc, p.cmin), p.cmax);
-    stv<DT>(p.y, ((long long)(plane0 + pp) * p.OH + oh0 + orow) * p.OW + ow, acc);
+    const long long yi = ((long long)(plane0 + pp) * p.OH + oh0 + orow) * p.OW + ow;
+    if (p.res) acc = p.rcs * acc + p.rrs * ldv<DT>(p.res, yi);
+    stv<DT>(p.y, yi, acc);
   }
 }
 
@@ -188,6 +192,8 @@ struct DwFast {
   int has_clamp;
   int act;
   float cmin, cmax;
+  const void* res;  // residual (output-shaped) or null: y = rcs * y + rrs * res
+  float rcs, rrs;
 };
 
 __device__ __forceinline__ void unpack(const uint4& v, float* f, std::integral_constant<int, WGX_FLOAT32>) {
@@ -381,15 +387,16 @@ __global__ __launch_bounds__(NT) void k_dw_fast(DwFast p) {
 #pragma unroll
         for (int o = 0; o < OV; ++o) acc[o] = fmaf(win[o * S + kw], wv[kh * K + kw], acc[o]);
     }
+    const long long yo = ((long long)(plane0 + pp) * p.OH + oh0 + orow) * p.OW + ow0;
     uint32_t h[OV];
 #pragma unroll
     for (int o = 0; o < OV; ++o) {
       float v = acc[o];
       v = apply_act(p.act, v);
       if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
+      if (p.res && ow0 + o < p.OW) v = p.rcs * v + p.rrs * ldv<DT>(p.res, yo + o);
       h[o] = to_bits<DT>(v);
     }
-    const long long yo = ((long long)(plane0 + pp) * p.OH + oh0 + orow) * p.OW + ow0;
     char* yp = static_cast<char*>(p.y) + yo * ES;
     const uintptr_t ya = reinterpret_cast<uintptr_t>(yp);
     if (ow0 + OV <= p.OW && (ya & 15) == 0 && (OV * ES) % 16 == 0) {
@@ -449,6 +456,8 @@ struct DwReg {
   int has_clamp;
   int act;
   float cmin, cmax;
+  const void* res;  // residual (output-shaped) or null: y = rcs * y + rrs * res
+  float rcs, rrs;
 };
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -541,6 +550,40 @@ __global__ __launch_bounds__(64) void k_dw_reg(DwReg p) {
     }
   }
 
+  // 1b. the residual's output rows (the same offsets as the stores below),
+  //     issued now so their latency hides under the stencil
+  constexpr int OD = OV / 2;
+  uint32_t rres[R][OD];
+  const int nvalid = active ? min(OV, p.OW - seg * OV) : 0;
+  if (p.res) {
+    const rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(static_cast<const char*>(p.res)) + yb0, 0,
+                                                        (int)(yl > 0x7fffffffull ? 0x7fffffffull : yl), 0x00020000);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int oh = oh0 + r;
+      const uint32_t off = (uint32_t)(((ps * p.OH + oh) * p.OW + seg * OV) * 2);
+      const bool rok = oh < p.OH;
+      if (nvalid == OV) {
+        if constexpr (OV == 8) {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(rr, (int)(rok ? off : OOB), 0, 0);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) rres[r][d] = v[d];
+        } else {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b64(rr, (int)(rok ? off : OOB), 0, 0);
+          rres[r][0] = v[0];
+          rres[r][1] = v[1];
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < OD; ++d) {
+          const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rr, (int)(rok && 2 * d < nvalid ? off + 4 * d : OOB), 0, 0);
+          const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(rr, (int)(rok && 2 * d + 1 < nvalid ? off + 4 * d + 2 : OOB), 0, 0);
+          rres[r][d] = lo | (hi << 16);
+        }
+      }
+    }
+  }
+
   // 2. weights of this lane's plane: packed pairs (w[kw], w[kw+1]) starting at
   //    even and at odd kw, and the two taps that can be left over, in fp32
   uint32_t wpe[K][NP], wpo[K][NP];
@@ -610,7 +653,6 @@ __global__ __launch_bounds__(64) void k_dw_reg(DwReg p) {
 
   // 4. stores: OV halves per output row, one vector store when whole
   if (!active) return;
-  const int nvalid = min(OV, p.OW - seg * OV);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int oh = oh0 + r;
@@ -621,6 +663,7 @@ __global__ __launch_bounds__(64) void k_dw_reg(DwReg p) {
       float v = acc[r][o];
       v = apply_act(p.act, v);
       if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
+      if (p.res) v = p.rcs * v + p.rrs * ((o & 1) ? hi_f(rres[r][o / 2]) : lo_f(rres[r][o / 2]));
       h[o] = __builtin_bit_cast(uint16_t, (_Float16)v);
     }
     const uint32_t off = (uint32_t)(((ps * p.OH + oh) * p.OW + seg * OV) * 2);
@@ -649,6 +692,7 @@ bool plan_reg(const DwDesc& d, DwReg& p, int& ov, int& R, long long& blocks) {
       d.pH != K / 2 || d.pW != K / 2 || d.dH != 1 || d.dW != 1)
     return false;
   if ((d.IW & 1) || (d.OW & 1) || (reinterpret_cast<uintptr_t>(d.x) & 3) || (reinterpret_cast<uintptr_t>(d.y) & 3) ||
+      (reinterpret_cast<uintptr_t>(d.res) & 3) ||
       (d.w && (reinterpret_cast<uintptr_t>(d.w) & 1)))
     return false;
   const int S = d.sH;
@@ -693,6 +737,9 @@ bool plan_reg(const DwDesc& d, DwReg& p, int& ov, int& R, long long& blocks) {
   p.act = d.act;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
+  p.res = d.res;
+  p.rcs = d.res_conv_scale;
+  p.rrs = d.res_scale;
   blocks = p.units;
   return true;
 }
@@ -844,6 +891,9 @@ bool plan_fast(const DwDesc& d, DwFast& p, int& ov, int& blocks, size_t& lds) {
   p.act = d.act;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
+  p.res = d.res;
+  p.rcs = d.res_conv_scale;
+  p.rrs = d.res_scale;
   return (long long)p.ppb * d.IH * d.IW < (1LL << 30);
 }
 
@@ -890,6 +940,9 @@ hipError_t launch_depthwise(const DwDesc& d, hipStream_t s, std::string* name) {
   p.act = d.act;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
+  p.res = d.res;
+  p.rcs = d.res_conv_scale;
+  p.rrs = d.res_scale;
   p.nplanes = d.B * d.C;
   // LDS row width: every column any output touches, iw in [-pW, (OW-1)sW - pW + (KW-1)dW].
   p.lw = (d.OW - 1) * d.sW + (d.KW - 1) * d.dW + 1;

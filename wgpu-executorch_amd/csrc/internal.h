@@ -90,6 +90,10 @@ struct DwDesc {
   int has_clamp;
   int act;  // WGX_ACT_*: applied after the bias, before the clamp
   float cmin, cmax;
+  // optional residual of the output's shape, added after the clamp:
+  // y = res_conv_scale * y + res_scale * res (null: none)
+  const void* res;
+  float res_conv_scale, res_scale;
 };
 hipError_t launch_depthwise(const DwDesc& d, hipStream_t s, std::string* name);
 

@@ -504,9 +504,11 @@ int wgx_record_bmm(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const w
 
 // ------------------------------------------------------------------ convolution
 
-int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight,
-                      const wgx_tensor* bias, const wgx_conv_args* args, const wgx_tensor* out) {
-  CTX_GUARD(c);
+// res (checked by the caller): an output-shaped tensor added after the
+// epilogue, y = rcs * y + rrs * res; depthwise convolutions only.
+static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight, const wgx_tensor* bias,
+                       const wgx_conv_args* args, const wgx_tensor* res, float rcs, float rrs,
+                       const wgx_tensor* out) {
   int r;
   if (!args) return c->fail(WGX_ERR_INVALID, "convolution: args is NULL");
   if ((r = c->check(in, "convolution: input")) || (r = c->check(weight, "convolution: weight")) ||
@@ -594,10 +596,15 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
     d.act = act;
     d.cmin = cmin;
     d.cmax = cmax;
+    d.res = res ? res->data : nullptr;
+    d.res_conv_scale = rcs;
+    d.res_scale = rrs;
     e = launch_depthwise(d, c->dry(), &name);
     if (e == hipSuccess) return c->push([d](hipStream_t s) { return launch_depthwise(d, s, nullptr); }, name);
     // bands too wide for LDS: fall through to the direct kernel
   }
+  if (res)
+    return c->fail(WGX_ERR_INVALID, "convolution: a residual is supported on depthwise convolutions only");
   const ConvGeom geom{(int)IH, (int)IW, (int)OW, sH, sW, pH, pW, (int)KH, (int)KW, dH, dW};
   const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0;
   const bool gemm_ok = !args->transposed && groups == 1 &&
@@ -676,6 +683,34 @@ int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight
   e = launch_direct_conv(d, c->dry(), &name);
   if (e != hipSuccess) return c->hip_fail(e, "kernel set-up");
   return c->push([d](hipStream_t s) { return launch_direct_conv(d, s, nullptr); }, name);
+}
+
+int wgx_record_conv2d(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight,
+                      const wgx_tensor* bias, const wgx_conv_args* args, const wgx_tensor* out) {
+  CTX_GUARD(c);
+  return record_conv(c, in, weight, bias, args, nullptr, 1.0f, 0.0f, out);
+}
+
+int wgx_record_conv2d_residual(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weight,
+                               const wgx_tensor* bias, const wgx_conv_args* args,
+                               const wgx_tensor* residual, float conv_scale, float residual_scale,
+                               const wgx_tensor* out) {
+  CTX_GUARD(c);
+  int r;
+  if (!residual) return c->fail(WGX_ERR_INVALID, "convolution: residual is NULL");
+  if ((r = c->check(residual, "convolution: residual")) || (r = c->check(out, "convolution: output"))) return r;
+  if (residual->dtype != out->dtype || residual->ndim != out->ndim)
+    return c->fail(WGX_ERR_INVALID, "convolution: residual must match the output's dtype and shape");
+  for (int i = 0; i < out->ndim; ++i)
+    if (residual->shape[i] != out->shape[i])
+      return c->fail(WGX_ERR_INVALID, "convolution: residual must match the output's dtype and shape");
+  // element i of the output reads element i of the residual: the same
+  // memory is fine, a shifted overlap is not
+  const uintptr_t rb = reinterpret_cast<uintptr_t>(residual->data), ob = reinterpret_cast<uintptr_t>(out->data);
+  const uintptr_t bytes = (uintptr_t)numel(out) * elsize(out->dtype);
+  if (rb != ob && rb < ob + bytes && ob < rb + bytes)
+    return c->fail(WGX_ERR_INVALID, "convolution: residual partly overlaps the output");
+  return record_conv(c, in, weight, bias, args, residual, conv_scale, residual_scale, out);
 }
 
 // ------------------------------------------------------------------ simple ops

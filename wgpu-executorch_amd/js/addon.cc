@@ -303,6 +303,16 @@ napi_value record_conv2d(napi_env env, napi_callback_info info) {
   ca.clamp_min = (float)num(env, prop(env, o, "clampMin"));
   ca.clamp_max = (float)num(env, prop(env, o, "clampMax"));
   ca.activation = i32(env, prop(env, o, "activation"));  // absent: 0, no activation
+  napi_value rv = prop(env, o, "residual");  // absent / null: no residual
+  if (!is_nullish(env, rv)) {
+    wgx_tensor tr;
+    if (!to_tensor(env, rv, tr)) return nullptr;
+    if (!ok(env, c, wgx_record_conv2d_residual(c, &tin, &tw, has_bias ? &tb : nullptr, &ca, &tr,
+                                               (float)num(env, prop(env, o, "convScale")),
+                                               (float)num(env, prop(env, o, "residualScale")), &to)))
+      return nullptr;
+    return undefined(env);
+  }
   if (!ok(env, c, wgx_record_conv2d(c, &tin, &tw, has_bias ? &tb : nullptr, &ca, &to))) return nullptr;
   return undefined(env);
 }

@@ -329,29 +329,42 @@ class WgpuExecutionContext {
     let fused = new Map();
     if (fuse) {
       const triples = siluTriples(program);
-      // A memory plan may give the product y the space of an input of the
-      // convolution that is dead after it (the unfused mul reads only c and
-      // s).  The fused launch would then overwrite data it still reads, so
-      // such a y, when it is not part of a view group, moves to memory of
-      // its own: one buffer for all of them.
-      const moved = triples.filter((t) => !views.place.has(t.y) &&
-        convReads(program, t.k, tensors).some((r) => overlaps(r, tensors.get(t.y))));
-      const movedBytes = moved.reduce((n, t) => n + align(Math.max(4, tensors.get(t.y).byteLength)), 0);
+      // The fused launch writes the last tensor of the group (y, or z with a
+      // residual) while it reads the convolution's input, weight and bias
+      // (and the residual, element for element).  A memory plan may give that
+      // output the space of an input that is dead after it (the unfused ops
+      // never read it then), so such an output, when it is not part of a view
+      // group, moves to memory of its own: one buffer for all of them.
+      const outOf = (t) => (t.add ? t.add.z : t.y);
+      const clash = (t) => {
+        const to = tensors.get(outOf(t));
+        if (convReads(program, t.k, tensors).some((r) => overlaps(r, to))) return true;
+        if (!t.add) return false;
+        const tr = tensors.get(t.add.r);
+        return tr.buffer.ptr !== to.buffer.ptr && overlaps(tr, to);  // the same memory is fine
+      };
+      const moved = triples.filter((t) => !views.place.has(outOf(t)) && clash(t));
+      const movedBytes = moved.reduce((n, t) => n + align(Math.max(4, tensors.get(outOf(t)).byteLength)), 0);
       if (movedBytes > 0) {
         const slab = this.storageBuffer(movedBytes);
         let at = 0;
         for (const t of moved) {
-          const ty = tensors.get(t.y);
-          tensors.set(t.y, this.tensor(ty.dtype, ty.shape, slab.view(at, ty.byteLength)));
-          at += align(Math.max(4, ty.byteLength));
+          const to = tensors.get(outOf(t));
+          tensors.set(outOf(t), this.tensor(to.dtype, to.shape, slab.view(at, to.byteLength)));
+          at += align(Math.max(4, to.byteLength));
         }
       }
       for (const t of triples) {
-        const ty = tensors.get(t.y);
-        if (convReads(program, t.k, tensors).some((r) => overlaps(r, ty))) continue;
+        if (clash(t)) continue;
         const fargs = resolveArgs(program.chain[t.k], program.values, tensors);
-        fargs[fargs.length - 1] = ty;
-        fused.set(t.k, fargs);
+        fargs.pop();
+        if (t.add) {
+          fargs.push(tensors.get(t.add.r), t.add.convScale, t.add.residualScale, tensors.get(t.add.z));
+          fused.set(t.k, { shader: shaders.convolutionSiluAdd, args: fargs, ops: 4 });
+        } else {
+          fargs.push(tensors.get(t.y));
+          fused.set(t.k, { shader: shaders.convolutionSilu, args: fargs, ops: 3 });
+        }
       }
     }
 
@@ -366,9 +379,9 @@ class WgpuExecutionContext {
     for (let k = 0; k < program.chain.length; k++) {
       if (views.elided.has(k)) continue;  // its output already is its inputs' bytes
       const f = fused.get(k);
-      if (f !== undefined) {  // conv -> sigmoid -> mul as one convolution with the SiLU epilogue
-        this.recordShader(shaders.convolutionSilu, f);
-        k += 2;
+      if (f !== undefined) {  // conv -> sigmoid -> mul (-> add) as one convolution launch
+        this.recordShader(f.shader, f.args);
+        k += f.ops - 1;
         continue;
       }
       const op = program.chain[k];
@@ -497,8 +510,12 @@ function convReads(program, k, tensors) {
  * sigmoid(c) -> s, mul(c, s) -> y, three consecutive ops.  When c and s are
  * read by nothing else (and are not program outputs) the convolution can
  * write SiLU(conv) straight into y, one launch instead of three and two
- * feature-map round trips fewer.  Returns the triples as {k, y}: k the
- * convolution's chain index, y the product.
+ * feature-map round trips fewer.  When the next op is aten.add.Tensor with y
+ * as one operand (and y read by nothing else) on a depthwise convolution, the
+ * add joins too: the depthwise kernels add an output-shaped residual in their
+ * epilogue.  Returns {k, y, add}: k the convolution's chain index, y the
+ * product, add null or {k, r, z, convScale, residualScale} with z = the add's
+ * output = convScale * y + residualScale * r.
  */
 function siluTriples(program) {
   const { chain, values } = program;
@@ -513,8 +530,27 @@ function siluTriples(program) {
     const c = conv.args[conv.args.length - 1], s = sig.args[1], y = mul.args[2];
     if (sig.args[0] !== c || !((mul.args[0] === c && mul.args[1] === s) || (mul.args[0] === s && mul.args[1] === c))) continue;
     if (uses.get(c) !== 3 || uses.get(s) !== 2 || !same(values[c], values[y])) continue;
-    out.push({ k, y });
-    k += 2;
+    const t = { k, y, add: null };
+    // aten.add.Tensor(a, b, alpha) -> z right after, with y one operand and
+    // read by nothing else, on a depthwise convolution: the residual epilogue
+    const add = chain[k + 3];
+    if (add && add.name === 'aten.add.Tensor' && add.args.length === 4 && uses.get(y) === 2 &&
+        (add.args[0] === y) !== (add.args[1] === y)) {
+      const r = add.args[0] === y ? add.args[1] : add.args[0];
+      const av = values[add.args[2]];
+      const alpha = av && av.type === 'scalar' ? Number(av.value) : 1;
+      const w = values[conv.args[1]], xin = values[conv.args[0]];
+      const groups = values[conv.args[8]] && values[conv.args[8]].type === 'scalar' ? values[conv.args[8]].value : 1;
+      const transposed = values[conv.args[6]] && values[conv.args[6]].value;
+      const depthwise = !transposed && w && xin && w.shape.length === 4 && xin.shape.length === 4 &&
+        w.shape[1] === 1 && w.shape[0] === groups && xin.shape[1] === groups;
+      if (depthwise && Number.isFinite(alpha) && same(values[r], values[y]) && same(values[add.args[3]], values[y])) {
+        t.add = { k: k + 3, r, z: add.args[3],
+          convScale: add.args[1] === y ? alpha : 1, residualScale: add.args[1] === y ? 1 : alpha };
+      }
+    }
+    out.push(t);
+    k += t.add ? 3 : 2;
   }
   return out;
 }

@@ -120,8 +120,10 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
   // ---------------------------------------------------------------- convolution (src/shaders/convolution/index.ts:58-310)
   // activation: 0 none, 1 SiLU folded into the epilogue (recordProgram's
   // conv -> sigmoid -> mul fusion; the reference operators never pass it)
+  // residual: {tensor, convScale, residualScale} adds an output-shaped tensor
+  // after the epilogue (recordProgram's folding of a following add)
   function recordConv(name, ctx, inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding,
-    groups, outTensor, clampMin, clampMax, activation) {
+    groups, outTensor, clampMin, clampMax, activation, residual) {
     if (!isFloatPair(inTensor) || weight.dtype !== inTensor.dtype || outTensor.dtype !== inTensor.dtype) {
       throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
     }
@@ -169,6 +171,9 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
       clampMin: clampMin === undefined ? -Infinity : clampMin,
       clampMax: clampMax === undefined ? Infinity : clampMax,
       activation: activation || 0,
+      residual: residual ? residual.tensor._c() : null,
+      convScale: residual ? residual.convScale : 1,
+      residualScale: residual ? residual.residualScale : 0,
     }, outTensor._c());
   }
 
@@ -180,6 +185,26 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
       const [inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding, groups, outTensor] = args;
       recordConv('aten.convolution.default', ctx, inTensor, weight, bias, stride, padding, dilation, transposed,
         outputPadding, groups, outTensor, undefined, undefined, 1);
+    },
+  };
+
+  /**
+   * aten.convolution.default, SiLU, then aten.add.Tensor with an
+   * output-shaped tensor, in one launch (depthwise convolutions):
+   * out = convScale * silu(conv) + residualScale * residual.
+   */
+  const convolutionSiluAdd = {
+    name: 'wgx.convolution_silu_add',
+    code: { depthwise: 'the depthwise kernels with the SiLU and residual epilogue' },
+    recordIn(ctx, args) {
+      const [inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding, groups, residual,
+        convScale, residualScale, outTensor] = args;
+      if (residual.dtype !== outTensor.dtype || residual.shape.length !== outTensor.shape.length ||
+          residual.shape.some((d, i) => d !== outTensor.shape[i])) {
+        throw new Error('wgx.convolution_silu_add: residual must match the output dtype and shape');
+      }
+      recordConv('aten.convolution.default', ctx, inTensor, weight, bias, stride, padding, dilation, transposed,
+        outputPadding, groups, outTensor, undefined, undefined, 1, { tensor: residual, convScale, residualScale });
     },
   };
 
@@ -359,7 +384,7 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
   return {
     add, sub, mul, sigmoid, relu, hardswish,
     mm, addmm, linear, bmm,
-    convolution, convWithClamp, convolutionSilu, maxPool2d,
+    convolution, convWithClamp, convolutionSilu, convolutionSiluAdd, maxPool2d,
     upsampleNearest2d,
     cat, splitWithSizesCopy,
     viewCopy: flatCopy('aten.view_copy.default'),

@@ -86,6 +86,8 @@ SIGNATURES = {
     "wgx_record_mm": (_I, [_P, _T, _T, _T, _T, ctypes.c_float, ctypes.c_float, ctypes.c_uint32]),
     "wgx_record_bmm": (_I, [_P, _T, _T, _T, ctypes.c_uint32]),
     "wgx_record_conv2d": (_I, [_P, _T, _T, _T, ctypes.POINTER(CConvArgs), _T]),
+    "wgx_record_conv2d_residual": (_I, [_P, _T, _T, _T, ctypes.POINTER(CConvArgs), _T, ctypes.c_float,
+                                        ctypes.c_float, _T]),
     "wgx_record_add": (_I, [_P, _T, _T, ctypes.c_float, _I, _T]),
     "wgx_record_mul": (_I, [_P, _T, _T, _T]),
     "wgx_record_unary": (_I, [_P, _I, _T, _T]),
@@ -288,7 +290,10 @@ class Context:
 
     def convolution(self, x: Tensor, w: Tensor, bias: Optional[Tensor], stride=(1, 1),
                     padding=(0, 0), dilation=(1, 1), transposed=False, output_padding=(0, 0),
-                    groups=1, out: Optional[Tensor] = None, clamp=None, activation: int = ACT_NONE) -> "Context":
+                    groups=1, out: Optional[Tensor] = None, clamp=None, activation: int = ACT_NONE,
+                    residual: Optional[Tensor] = None, conv_scale: float = 1.0,
+                    residual_scale: float = 1.0) -> "Context":
+        """residual: out = conv_scale * conv + residual_scale * residual (depthwise only)."""
         def hw(v):
             v = list(v) if isinstance(v, (list, tuple)) else [v]
             if len(v) == 1:
@@ -310,6 +315,13 @@ class Context:
         a.activation = int(activation)
         cx, cw, co = x.c(), w.c(), out.c()
         cb = bias.c() if bias is not None else None
+        if residual is not None:
+            cr = residual.c()
+            self._check(lib().wgx_record_conv2d_residual(self.h, ctypes.byref(cx), ctypes.byref(cw),
+                                                         ctypes.byref(cb) if cb is not None else None,
+                                                         ctypes.byref(a), ctypes.byref(cr), conv_scale,
+                                                         residual_scale, ctypes.byref(co)))
+            return self
         self._check(lib().wgx_record_conv2d(self.h, ctypes.byref(cx), ctypes.byref(cw),
                                             ctypes.byref(cb) if cb is not None else None,
                                             ctypes.byref(a), ctypes.byref(co)))
