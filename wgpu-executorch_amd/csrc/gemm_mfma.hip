@@ -1411,7 +1411,7 @@ hipError_t launch_nk(const KParams& kp, int batch, hipStream_t s) {
 // sums in LDS and each wave finishes a share of the tile's register groups:
 // the W partials are added in wave order (fixed, so the result does not
 // depend on timing), then bias, activation, clamp and one rounding.
-template <int DT, int BMODE, int TM, int TN, int W>
+template <int DT, int BMODE, int TM, int TN, int W, bool SA>
 __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
   constexpr int ES = DT == DT_F32 ? 4 : 2;
   constexpr int EPC = 16 / ES;     // elements per 16-byte chunk
@@ -1420,7 +1420,11 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
   constexpr int BM = TM * 32, BN = TN * 32;
   constexpr bool CONV = BMODE == B_CONV;
   constexpr bool NK = BMODE == B_NK;
-  extern __shared__ uint4 ws_lds[];  // tap table (B_CONV), then partials [W][NG][64] float4
+  static_assert(SA || !NK, "[N, K] rows are always staged");
+  constexpr int AROWS = SA ? TM * 32 + (NK ? TN * 32 : 0) : 0;  // rows staged per wave: A, and B for [N, K]
+  // LDS: tap table (B_CONV) | per wave, its A (and [N, K] B) rows of one
+  // slice (AROWS x 128 B, swizzled) | partial sums [W][NG][64] float4
+  extern __shared__ uint4 ws_lds[];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1436,7 +1440,8 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
   const int m0 = (rt % tiles_m) * BM, n0 = (rt / tiles_m) * BN;
 
   const uint32_t* ktab = reinterpret_cast<const uint32_t*>(ws_lds);
-  float4* part = reinterpret_cast<float4*>(ws_lds + (CONV ? KT * BK / 4 : 0));
+  char* stage = reinterpret_cast<char*>(ws_lds + (CONV ? KT * BK / 4 : 0)) + wave * AROWS * 128;
+  float4* part = reinterpret_cast<float4*>(ws_lds + (CONV ? KT * BK / 4 : 0) + W * AROWS * 8);
 
   const int fr = lane & 31, fc = lane >> 5;
   const int mrows = min(BM, M - m0);
@@ -1448,12 +1453,21 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
                                CONV ? p.b_bytes
                                : NK ? (uint32_t)((long long)(N - 1) * p.ldb + K) * ES
                                     : (uint32_t)((long long)(K - 1) * p.ldb + N) * ES);
-  uint32_t aoff[TM];
-  bool aok[TM];
+  // SA: rows of A (and of a [N, K] B) are loaded coalesced, 8 lanes per
+  // row's 128-byte slice, 8 rows per load instruction, and reach the MFMA
+  // layout through the wave's LDS patch.  Without it each lane loads its MFMA
+  // fragment directly (lane = row), 16 bytes from its own cache line: 64
+  // lines per instruction, which measured as the address-FIFO bound of this
+  // kernel on long K ranges and in fp32; on short fp16 ranges the LDS round
+  // trip costs more than it saves.
+  const int lr = lane >> 3, lc = lane & 7;  // row within 8, 16-byte chunk
+  uint32_t aoff[TM * 4];
+  bool aok[TM * 4];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    aok[i] = i * 32 + fr < mrows;
-    aoff[i] = (uint32_t)((i * 32 + fr) * p.lda) * ES;
+  for (int q = 0; q < TM * 4; ++q) {
+    const int row = SA ? q * 8 + lr : (q >> 2) * 32 + fr;
+    aok[q] = row < mrows;
+    aoff[q] = (uint32_t)(row * p.lda + (SA ? lc * EPC : 0)) * ES;
   }
   // per column: base offset of the output pixel's window and the mask of the
   // kernel taps that land inside the image (zero past N: every load reads 0)
@@ -1492,17 +1506,24 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
     }
   }
   struct Frag {
-    uint4 a[TM][4];
+    uint4 a[TM * 4];                  // SA: row q*8 + lr, chunk lc; else MFMA fragment [i][kk] at i*4 + kk
     uint32_t b[TN][4][NK ? 1 : EPC];  // gathered elements
-    uint4 bv[TN][NK ? 4 : 1];         // [N, K] rows: one chunk per k-step
+    uint4 bv[NK ? TN * 4 : 1];        // [N, K] rows, as A
   };
   // slice s: per k-step kk (16 bytes of k per lane), the lane's chunk kk*2+fc
   auto loadA = [&](Frag& F, int s) {
+    if constexpr (SA) {
+      const int kc = s * BK + lc * EPC;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int kc = s * BK + (kk * 2 + fc) * EPC;
+      for (int q = 0; q < TM * 4; ++q) F.a[q] = ld_b128(ra, (aok[q] && kc < K) ? aoff[q] + (uint32_t)(s * BK) * ES : OOB);
+    } else {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) F.a[i][kk] = ld_b128(ra, (aok[i] && kc < K) ? aoff[i] + (uint32_t)kc * ES : OOB);
+      for (int kk = 0; kk < 4; ++kk) {
+        const int kc = s * BK + (kk * 2 + fc) * EPC;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          F.a[i * 4 + kk] = ld_b128(ra, (aok[i * 4] && kc < K) ? aoff[i * 4] + (uint32_t)kc * ES : OOB);
+      }
     }
   };
   auto loadB = [&](Frag& F, int s) {
@@ -1533,9 +1554,14 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
             F.b[j][kk][e] = ES == 4 ? ld_b32(rbs, off) : ld_b16(rbs, off);
           }
       } else if constexpr (NK) {
+        if (kk == 0) {  // the [N, K] rows of the slice, coalesced like A
+          const int kr = s * BK + lc * EPC;
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          F.bv[j][kk] = ld_b128(rbs, (cmask[j] && kc < K) ? (uint32_t)(colbase[j] * p.ldb + kc) * ES : OOB);
+          for (int q = 0; q < TN * 4; ++q) {
+            const int n = n0 + q * 8 + lr;
+            F.bv[q] = ld_b128(rbs, (n < N && kr < K) ? (uint32_t)(n * p.ldb + kr) * ES : OOB);
+          }
+        }
       } else {
 #pragma unroll
         for (int j = 0; j < TN; ++j)
@@ -1559,20 +1585,40 @@ __global__ __launch_bounds__(W * 64) void k_gemm_ws(KParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   auto mma = [&](const Frag& F) {
+    // SA: this wave's rows -> LDS (coalesced layout), back in the MFMA
+    // layout: lane = row, chunk kk*2 + fc
+    uint4 af[TM][4];
+    if constexpr (SA) {
+#pragma unroll
+      for (int q = 0; q < TM * 4; ++q) *reinterpret_cast<uint4*>(stage + swz(q * 8 + lr, lc)) = F.a[q];
+      if constexpr (NK) {
+#pragma unroll
+        for (int q = 0; q < TN * 4; ++q) *reinterpret_cast<uint4*>(stage + swz(TM * 32 + q * 8 + lr, lc)) = F.bv[q];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) af[i][kk] = *reinterpret_cast<const uint4*>(stage + swz(i * 32 + fr, kk * 2 + fc));
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) af[i][kk] = F.a[i * 4 + kk];
+    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         uint4 bq;
         if constexpr (NK)
-          bq = F.bv[j][kk];
+          bq = *reinterpret_cast<const uint4*>(stage + swz(TM * 32 + j * 32 + fr, kk * 2 + fc));
         else if constexpr (ES == 4)
           bq = make_uint4(F.b[j][kk][0], F.b[j][kk][1], F.b[j][kk][2], F.b[j][kk][3]);
         else
           bq = make_uint4(pack2(F.b[j][kk][0], F.b[j][kk][1]), pack2(F.b[j][kk][2], F.b[j][kk][3]),
                           pack2(F.b[j][kk][4], F.b[j][kk][5]), pack2(F.b[j][kk][6], F.b[j][kk][7]));
 #pragma unroll
-        for (int i = 0; i < TM; ++i) acc[i][j] = mfma_frag<DT>(bq, F.a[i][kk], acc[i][j]);
+        for (int i = 0; i < TM; ++i) acc[i][j] = mfma_frag<DT>(bq, af[i][kk], acc[i][j]);
       }
   };
 
@@ -1819,12 +1865,14 @@ struct WsCfg {
 };
 constexpr WsCfg kWsCfgs[] = {{1, 1, 4}, {1, 1, 8}, {2, 1, 4}, {2, 1, 8}, {1, 2, 4}};
 
-template <int DT, int BMODE, int TM, int TN, int W>
+template <int DT, int BMODE, int TM, int TN, int W, bool SA>
 hipError_t launch_ws(const KParams& kp, int batch, hipStream_t s) {
-  auto fn = k_gemm_ws<DT, BMODE, TM, TN, W>;
+  auto fn = k_gemm_ws<DT, BMODE, TM, TN, W, SA>;
   constexpr int BK = DT == DT_F32 ? 32 : 64;
   const int kt = (kp.K + BK - 1) / BK;
-  const size_t dyn = (BMODE == B_CONV ? (size_t)kt * BK * 4 : 0) + (size_t)W * TM * TN * 4 * 64 * 16;
+  constexpr int AROWS = SA ? TM * 32 + (BMODE == B_NK ? TN * 32 : 0) : 0;
+  const size_t dyn = (BMODE == B_CONV ? (size_t)kt * BK * 4 : 0) + (size_t)W * AROWS * 128 +
+                     (size_t)W * TM * TN * 4 * 64 * 16;
   if (dyn > 160 * 1024) return hipErrorInvalidValue;
   static size_t attr_dyn = 0;  // largest dynamic size allowed so far
   if (dyn > attr_dyn && s != name_only()) {
@@ -1843,13 +1891,13 @@ hipError_t launch_ws(const KParams& kp, int batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int DT, int BMODE>
+template <int DT, int BMODE, bool SA>
 hipError_t dispatch_ws(const WsCfg& c, const KParams& kp, int batch, hipStream_t s) {
-  if (c.tm == 1 && c.tn == 1 && c.w == 4) return launch_ws<DT, BMODE, 1, 1, 4>(kp, batch, s);
-  if (c.tm == 1 && c.tn == 1 && c.w == 8) return launch_ws<DT, BMODE, 1, 1, 8>(kp, batch, s);
-  if (c.tm == 2 && c.tn == 1 && c.w == 4) return launch_ws<DT, BMODE, 2, 1, 4>(kp, batch, s);
-  if (c.tm == 2 && c.tn == 1 && c.w == 8) return launch_ws<DT, BMODE, 2, 1, 8>(kp, batch, s);
-  if (c.tm == 1 && c.tn == 2 && c.w == 4) return launch_ws<DT, BMODE, 1, 2, 4>(kp, batch, s);
+  if (c.tm == 1 && c.tn == 1 && c.w == 4) return launch_ws<DT, BMODE, 1, 1, 4, SA>(kp, batch, s);
+  if (c.tm == 1 && c.tn == 1 && c.w == 8) return launch_ws<DT, BMODE, 1, 1, 8, SA>(kp, batch, s);
+  if (c.tm == 2 && c.tn == 1 && c.w == 4) return launch_ws<DT, BMODE, 2, 1, 4, SA>(kp, batch, s);
+  if (c.tm == 2 && c.tn == 1 && c.w == 8) return launch_ws<DT, BMODE, 2, 1, 8, SA>(kp, batch, s);
+  if (c.tm == 1 && c.tn == 2 && c.w == 4) return launch_ws<DT, BMODE, 1, 2, 4, SA>(kp, batch, s);
   return hipErrorNotSupported;
 }
 
@@ -2036,13 +2084,21 @@ bool ws_choice(const GemmDesc& d, const Plan& pl, WsCfg* cfg) {
   } else {
     if (!pl.bvec || ((long long)(d.N - 1) * d.ldb + d.K) * pl.es >= (1LL << 31)) return false;
   }
+  // the configuration's LDS: tap table, per-wave row patches, partial sums
+  const auto fits = [&](const WsCfg& c) {
+    const int bk = pl.f32 ? 32 : 64, kt = (d.K + bk - 1) / bk;
+    const bool sa = pl.f32 || d.K >= 1024;  // as launch_gemm_mfma stages A
+    const size_t rows = sa ? 32 * c.tm + (d.bmode == B_NK ? 32 * c.tn : 0) : 0;
+    return (d.bmode == B_CONV ? (size_t)kt * bk * 4 : 0) + (size_t)c.w * rows * 128 +
+               (size_t)c.w * c.tm * c.tn * 4 * 1024 <= 160 * 1024;
+  };
   const char* force = getenv("WGX_WS");
   if (force) {
     if (strcmp(force, "off") == 0) return false;
     int tm = 0, tn = 0, w = 0;
     if (sscanf(force, "%dx%dw%d", &tm, &tn, &w) == 3)
       for (const WsCfg& c : kWsCfgs)
-        if (c.tm == tm && c.tn == tn && c.w == w) {
+        if (c.tm == tm && c.tn == tn && c.w == w && fits(c)) {
           *cfg = c;
           return true;
         }
@@ -2055,7 +2111,7 @@ bool ws_choice(const GemmDesc& d, const Plan& pl, WsCfg* cfg) {
   if (tiles32 <= cus) *cfg = WsCfg{1, 1, 8};
   else if (pl.f32) *cfg = WsCfg{2, 1, 4};
   else *cfg = tiles2 <= cus ? WsCfg{2, 1, 8} : WsCfg{2, 1, 4};
-  return true;
+  return fits(*cfg);
 }
 
 }  // namespace
@@ -2164,11 +2220,16 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
       *name = buf;
     }
     kp.tiles_n = (d.N + 32 * wc.tn - 1) / (32 * wc.tn);
-    if (d.bmode == B_CONV)
-      return f32 ? dispatch_ws<DT_F32, B_CONV>(wc, kp, d.batch, s) : dispatch_ws<DT_F16, B_CONV>(wc, kp, d.batch, s);
-    if (d.bmode == B_NK)
-      return f32 ? dispatch_ws<DT_F32, B_NK>(wc, kp, d.batch, s) : dispatch_ws<DT_F16, B_NK>(wc, kp, d.batch, s);
-    return f32 ? dispatch_ws<DT_F32, B_KN>(wc, kp, d.batch, s) : dispatch_ws<DT_F16, B_KN>(wc, kp, d.batch, s);
+    // A rows staged through LDS: fp32 always, fp16 on long K ranges
+    // (measured on MI355X: ahead from K = 1152, behind at K = 576)
+    if (d.bmode == B_CONV) {
+      if (f32) return dispatch_ws<DT_F32, B_CONV, true>(wc, kp, d.batch, s);
+      return d.K >= 1024 ? dispatch_ws<DT_F16, B_CONV, true>(wc, kp, d.batch, s)
+                         : dispatch_ws<DT_F16, B_CONV, false>(wc, kp, d.batch, s);
+    }
+    if (!f32) return hipErrorNotSupported;
+    if (d.bmode == B_NK) return dispatch_ws<DT_F32, B_NK, true>(wc, kp, d.batch, s);
+    return dispatch_ws<DT_F32, B_KN, true>(wc, kp, d.batch, s);
   }
   const bool knv = d.bmode == B_KN && bvec;
   if (name) {
