@@ -88,6 +88,13 @@ def test_mm_validation(hctx, pkg):
     assert hctx.last_kernel.startswith("gemm_mfma_f16") and "_kn" in hctx.last_kernel
     hctx.mm(h[0], hctx.tensor("float16", [80, 96]), h[2], trans_b=True)
     assert hctx.last_kernel.endswith("nk")
+    # the config-4 addmm shape: large tiles in both weight layouts, a [K, N]
+    # weight through the [N, K] staging pass
+    big = [hctx.tensor("float16", s) for s in ([4096, 768], [768, 3072], [4096, 3072])]
+    hctx.mm(*big)
+    assert hctx.last_kernel == "gemm_mfma_f16_256x192w4_kn2nk_big", hctx.last_kernel
+    hctx.mm(big[0], hctx.tensor("float16", [3072, 768]), big[2], trans_b=True)
+    assert hctx.last_kernel == "gemm_mfma_f16_256x192w4_nk_big", hctx.last_kernel
     with pytest.raises(E, match="bias"):
         hctx.mm(*h, bias=hctx.tensor("float16", [7]))
 

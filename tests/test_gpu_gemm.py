@@ -177,6 +177,64 @@ def test_large_tile_kernel_edges(gpu_ctx, orc, pkg, tile, monkeypatch):
     assert_parity(to.get_f32(), ref, refa, "float16", 72, f"big bmm {tile} {kernel}")
 
 
+@pytest.mark.parametrize("tile", ["256x192b", "192x256b"])
+def test_kn_operand_staged_for_large_tile_kernel(gpu_ctx, orc, pkg, tile, monkeypatch):
+    """A [K, N] B on the large-tile kernel: rewritten as [N, K] by the staging
+    pass, then multiplied by the [N, K] kernel.  Ragged tiles in M, N and K
+    (partial 64 x 64 staging tiles), a batch, alpha / beta, both 16-bit
+    types; the result must carry the same bits as the [N, K] form of the
+    same product and be within the fp16 bound of the fp64 oracle."""
+    I = pkg.inputs
+    monkeypatch.setenv("WGX_MFMA_TILE", tile)
+    for i, (M, N, K) in enumerate([(300, 200, 104), (513, 392, 136), (256, 192, 32), (70, 8, 2056)]):
+        for dtype in ("float16", "bfloat16"):
+            A = round_in(I.uniform(2400 + i, (M, K), -1, 1), dtype)
+            B = round_in(I.uniform(2500 + i, (K, N), -1, 1), dtype)
+            bias = round_in(I.uniform(2600 + i, (N,), -0.5, 0.5), dtype)
+            alpha, beta = (0.5, 2.0) if i % 2 else (1.0, 1.0)
+            nn, k_nn = run_mm(gpu_ctx, A, B, dtype, bias=bias, alpha=alpha, beta=beta)
+            nt, k_nt = run_mm(gpu_ctx, A, np.ascontiguousarray(B.T), dtype, bias=bias, trans_b=True,
+                              alpha=alpha, beta=beta)
+            assert k_nn.endswith("_kn2nk_big") and tile[:-1] in k_nn, k_nn
+            assert k_nt.endswith("w4_nk_big"), k_nt
+            ref, refa = orc.gemm_f64(A, B)
+            ref = alpha * ref + beta * bias
+            refa = abs(alpha) * refa + abs(beta) * np.abs(bias)
+            assert_parity(nn, ref, refa, dtype, K, f"staged {tile} {dtype} {M}x{N}x{K} {k_nn}")
+            assert np.array_equal(nn, nt), f"staged {tile} {dtype} {M}x{N}x{K}: [K,N] != [N,K] bits"
+    # a batch of [K, N] right operands
+    A = round_in(I.uniform(2700, (3, 260, 72), -1, 1), "float16")
+    B = round_in(I.uniform(2701, (3, 72, 200), -1, 1), "float16")
+    ta, tbb = gpu_ctx.from_numpy(A, "float16"), gpu_ctx.from_numpy(B, "float16")
+    to = gpu_ctx.tensor("float16", [3, 260, 200])
+    gpu_ctx.reset()
+    gpu_ctx.bmm(ta, tbb, to)
+    kernel = gpu_ctx.last_kernel
+    gpu_ctx.submit()
+    gpu_ctx.sync()
+    assert kernel.endswith("_kn2nk_big"), kernel
+    ref, refa = orc.gemm_f64(A, B)
+    assert_parity(to.get_f32(), ref, refa, "float16", 72, f"staged bmm {tile} {kernel}")
+
+
+def test_config4_addmm_nn_takes_staged_large_tiles(gpu_ctx, orc, pkg):
+    """The config-4 addmm in aten.mm's own [K, N] weight layout runs the
+    staging pass and the large-tile kernel by default, and replays of the
+    recorded pair agree with its [N, K] form bit for bit."""
+    I = pkg.inputs
+    M, K, N = 4096, 768, 3072
+    X = round_in(I.normal(2800, (M, K)), "float16")
+    W = round_in(I.normal(2801, (K, N), 0, 0.02), "float16")
+    b = round_in(I.uniform(2802, (N,), -0.1, 0.1), "float16")
+    nn, k_nn = run_mm(gpu_ctx, X, W, "float16", bias=b)
+    assert k_nn.endswith("_kn2nk_big"), k_nn
+    nt, _ = run_mm(gpu_ctx, X, np.ascontiguousarray(W.T), "float16", bias=b, trans_b=True)
+    assert np.array_equal(nn, nt)
+    rows = sample_rows(M, 64)
+    ref, refa = orc.gemm_f64(X, W, b, rows=rows)
+    assert_parity(nn[rows], ref, refa, "float16", K, f"config4 NN {k_nn}")
+
+
 @pytest.mark.parametrize("cfg", ["1x1w4", "1x1w8", "2x1w4", "2x1w8", "1x2w4"])
 def test_wave_split_f32_gemm(gpu_ctx, orc, pkg, monkeypatch, cfg):
     """fp32 GEMMs with few tiles on every wave-split configuration: both B

@@ -1393,6 +1393,85 @@ hipError_t launch_nk(const KParams& kp, int batch, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ============================================================ [K,N] -> [N,K] staging
+// The large-tile kernel reads both operands k-contiguous.  A 16-bit [K, N]
+// operand (aten.mm's own layout) large enough for that kernel is first
+// rewritten as [N, K] into a workspace: one pass over B (2 x 2 bytes per
+// element through HBM, a few microseconds for a 768 x 3072 weight) buys the
+// large-tile loop, and the GEMM then computes on exactly the values the
+// [N, K] form would see, so both layouts give the same bits.
+//
+// One block moves a 64(k) x 64(n) tile: reads 128-byte row pieces of B
+// (8 lanes per row), parks them in LDS with a 66-element row pitch, and
+// writes 128-byte row pieces of B^T (8 lanes per row of 64 k).  With that
+// pitch the eight rows one gather step touches (8 apart) fall on eight
+// different bank groups, so the column reads are conflict free.
+__global__ __launch_bounds__(256) void k_kn_to_nk(const uint16_t* __restrict__ B, uint16_t* __restrict__ BT,
+                                                   int K, int N, long long ldb, long long sB, int tiles_k,
+                                                   int tiles_n) {
+  constexpr int P = 66;  // LDS row pitch in elements (132 bytes)
+  __shared__ __attribute__((aligned(16))) uint16_t t[64 * P];
+  const int tid = threadIdx.x;
+  const long long tk_tn = (long long)tiles_k * tiles_n;
+  const int z = (int)(blockIdx.x / tk_tn);
+  const int r = (int)(blockIdx.x % tk_tn);
+  const int k0 = (r / tiles_n) * 64, n0 = (r % tiles_n) * 64;
+  const uint16_t* src = B + (long long)z * sB;
+  uint16_t* dst = BT + (long long)z * N * K;
+  const bool vec = ((ldb & 7) == 0) && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i, row = c >> 3, q = c & 7;
+    const int k = k0 + row, n = n0 + q * 8;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (k < K) {
+      const uint16_t* p = src + (long long)k * ldb + n;
+      if (vec && n + 8 <= N) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < N) w[e >> 1] |= (uint32_t)p[e] << (16 * (e & 1));
+      }
+    }
+    uint32_t* lp = reinterpret_cast<uint32_t*>(t + row * P + q * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) lp[e] = w[e];
+  }
+  __syncthreads();
+  const bool ovec = ((K & 7) == 0) && ((reinterpret_cast<uintptr_t>(dst) & 15) == 0);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i, row = c >> 3, q = c & 7;  // row: n within the tile, q: 8 k
+    const int n = n0 + row, k = k0 + q * 8;
+    if (n >= N || k >= K) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = (uint32_t)t[(q * 8 + 2 * e) * P + row] | ((uint32_t)t[(q * 8 + 2 * e + 1) * P + row] << 16);
+    uint16_t* p = dst + (long long)n * K + k;
+    if (ovec && k + 8 <= K) {
+      *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (k + e < K) p[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
+hipError_t launch_kn_to_nk(const void* B, void* BT, int K, int N, long long ldb, long long sB, int batch,
+                           hipStream_t s) {
+  if (is_dry(s)) return hipSuccess;
+  const int tk = (K + 63) / 64, tn = (N + 63) / 64;
+  const long long grid = (long long)tk * tn * batch;
+  if (grid >= (1LL << 31)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_kn_to_nk, dim3((unsigned)grid), dim3(256), 0, s, static_cast<const uint16_t*>(B),
+                     static_cast<uint16_t*>(BT), K, N, ldb, sB, tk, tn);
+  return hipGetLastError();
+}
+
 // ============================================================ wave-split kernel
 // GEMMs with few output tiles -- convolutions as implicit im2col (B_CONV)
 // or 1x1 (B_KN, the input plane as a [K, N] operand), small mm / addmm in
@@ -1911,6 +1990,7 @@ constexpr Tile kTiles[] = {{256, 128, 4, 2},        {128, 256, 2, 4},        {25
                            {128, 64, 2, 2},         {64, 64, 2, 2}};
 
 bool use_v2();
+bool getenv_is0(const char* name);
 
 // LDS bytes of a block: three unpadded stages (pipelined kernel) or two padded
 // ones (register-staged kernel), the bias buffers and the im2col table.
@@ -1946,6 +2026,12 @@ Tile choose_tile(int M, int N, int K, int batch, bool avec, int bmode) {
     }
   }
   return bt;
+}
+
+// True when the environment variable is set to "0".
+bool getenv_is0(const char* name) {
+  const char* v = getenv(name);
+  return v && strcmp(v, "0") == 0;
 }
 
 bool use_v2() {
@@ -2002,6 +2088,7 @@ struct Plan {
   Tile t;
   bool pipelined;  // runs k_gemm3 (split-K capable)
   bool big;        // runs k_gemm_nk with tile bt
+  bool stage_b;    // big, on a [K, N] B rewritten as [N, K] first (k_kn_to_nk)
   Tile bt;
 };
 
@@ -2038,9 +2125,13 @@ Plan make_plan(const GemmDesc& d) {
     pl.pipelined = pl.avec && pl.bvec == (d.bmode != B_CONV) && !use_v2() &&
                    !(pl.t.bm == 256 && pl.t.bn == 256);
   if (pl.bf && d.bmode == B_CONV) pl.pipelined = false;
-  // the large-tile kernel for the [N, K] form when its tiles cost less
+  // the large-tile kernel for the [N, K] form when its tiles cost less; a
+  // 16-byte-aligned [K, N] B takes it too, through the [N, K] staging pass
+  // (WGX_KN_STAGE=0 keeps such GEMMs on k_gemm3)
   pl.big = false;
-  if (!pl.f32 && d.bmode == B_NK && pl.avec && pl.bvec && !use_v2()) {
+  pl.stage_b = false;
+  const bool kn_stage = d.bmode == B_KN && pl.bvec && (d.K % epc == 0) && !getenv_is0("WGX_KN_STAGE");
+  if (!pl.f32 && (d.bmode == B_NK || kn_stage) && pl.avec && pl.bvec && !use_v2()) {
     const int per_cu = pl.t.wgm * pl.t.wgn == 8 || tile_lds(pl.t, d.bmode, d.K) > 80 * 1024 ? 1 : 2;
     double best = tile_cost(pl.t, d.M, d.N, d.batch, per_cu);
     const char* force = getenv("WGX_MFMA_TILE");
@@ -2058,6 +2149,7 @@ Plan make_plan(const GemmDesc& d) {
         pl.bt = t;
       }
     }
+    pl.stage_b = pl.big && d.bmode == B_KN;
   }
   return pl;
 }
@@ -2120,6 +2212,12 @@ bool ws_choice(const GemmDesc& d, const Plan& pl, WsCfg* cfg) {
 // brings the units nearest to one per CU (so 200 tiles on 256 CUs stay
 // whole, 100 tiles become 300 units), each range at least 8 K slices long,
 // at most 8 ranges.
+size_t gemm_stage_b_bytes(const GemmDesc& d) {
+  if (d.dtype == WGX_FLOAT32) return 0;
+  const Plan pl = make_plan(d);
+  return pl.stage_b ? (size_t)d.batch * d.N * d.K * 2 : 0;
+}
+
 int gemm_split_plan(const GemmDesc& d, size_t* ws_bytes) {
   *ws_bytes = 0;
   const Plan pl = make_plan(d);
@@ -2200,8 +2298,18 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
     kp.tiles_n = (d.N + b.bn - 1) / b.bn;
     if (name) {
       char buf[96];
-      snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw4_nk_big", bf ? "bf16" : "f16", b.bm, b.bn);
+      snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw4_%snk_big", bf ? "bf16" : "f16", b.bm, b.bn,
+               pl.stage_b ? "kn2" : "");
       *name = buf;
+    }
+    if (pl.stage_b) {
+      // B [K, N] -> workspace [N, K] on the same stream, then the [N, K] kernel
+      if (!d.bt) return is_dry(s) ? hipSuccess : hipErrorInvalidValue;
+      const hipError_t e = launch_kn_to_nk(d.B, d.bt, d.K, d.N, d.ldb, d.sB, d.batch, s);
+      if (e != hipSuccess) return e;
+      kp.B = static_cast<const uint16_t*>(d.bt);
+      kp.ldb = d.K;
+      kp.sB = (long long)d.N * d.K;
     }
     // 128-byte LDS rows (8 full lines per DMA instruction) and two stages:
     // measured slightly ahead of 64-byte rows with five stages on MI355X

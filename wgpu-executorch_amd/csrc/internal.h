@@ -63,11 +63,17 @@ struct GemmDesc {
   // contiguous ranges; ws holds their fp32 partial sums, [splits][batch][M][N]
   int splits;
   float* ws;
+  // [N, K] copy of a 16-bit [K, N] B for the large-tile kernel
+  // (gemm_stage_b_bytes > 0): batch * N * K elements
+  void* bt;
 };
 
 // Split-K plan for an MFMA launch: how many K ranges (1 = none) and the
 // workspace size the launch then needs.
 int gemm_split_plan(const GemmDesc& d, size_t* ws_bytes);
+// Bytes of the [N, K] staging workspace the launch needs for its [K, N] B
+// (0: B is read in place).
+size_t gemm_stage_b_bytes(const GemmDesc& d);
 
 // Table rows needed for a B_CONV launch (K rounded up to the largest K tile).
 int conv_ktab_rows(int K);

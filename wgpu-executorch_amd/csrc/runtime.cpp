@@ -404,6 +404,12 @@ static int record_gemm(wgx_ctx* c, GemmDesc d) {
       if (!d.ws) return c->fail(WGX_ERR_OOM, "gemm: split-K workspace allocation failed");
       d.splits = splits;
     }
+    // a [K, N] B that the large-tile kernel reads as [N, K]: its staging copy
+    const size_t bt_bytes = gemm_stage_b_bytes(d);
+    if (bt_bytes > 0) {
+      d.bt = c->owned_alloc(bt_bytes);
+      if (!d.bt) return c->fail(WGX_ERR_OOM, "gemm: [N,K] staging workspace allocation failed");
+    }
   }
   if (!mfma) e = launch_gemm_f32(d, c->dry(), &name);
   else e = launch_gemm_mfma(d, c->dry(), &name);
