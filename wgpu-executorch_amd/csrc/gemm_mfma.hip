@@ -1075,43 +1075,61 @@ __attribute__((amdgpu_waves_per_eu((BM / WGM / 32) * (BN / WGN / 32) >= 8 ? 1 : 
                                 (uint32_t)((mrows - 1) * p.ldc + (N - n0)) * ES);
     const bool cvec = ((p.ldc & 3) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & (4 * ES - 1)) == 0) &&
                       ((p.sC & 3) == 0) && ((N & 3) == 0);
+    // Uniform epilogue choices hoisted out of the element loop: the plain
+    // forms (vector stores, no activation, no clamp; bias none / per column /
+    // per row) are straight-line code, everything else takes the general form.
+    const bool plain = p.act == WGX_ACT_NONE && !p.has_clamp && cvec;
+    const int emode = !plain ? 3 : (p.bias_mode == BIAS_COL ? 1 : (p.bias_mode == BIAS_ROW ? 2 : 0));
+    auto put = [&](auto mode) {
+      constexpr int MODE = decltype(mode)::value;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int row = wm * WM + i * 32 + frow;
-      const float rowb = p.bias_mode == BIAS_ROW ? sbias[par][row] : 0.0f;
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WM + i * 32 + frow;
+        float rowb = 0.0f;
+        if constexpr (MODE == 2) rowb = sbias[par][row];
+        if constexpr (MODE == 3) rowb = p.bias_mode == BIAS_ROW ? sbias[par][row] : 0.0f;
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col = wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
-          float4 bc = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (p.bias_mode == BIAS_COL) bc = *reinterpret_cast<const float4*>(&sbias[par][col]);
-          const float bb[4] = {bc.x, bc.y, bc.z, bc.w};
-          uint32_t h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
-            x = apply_act(p.act, x);
-            if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
-            if constexpr (DT == DT_F32) h[e] = __float_as_uint(x);
-            else h[e] = st_bits<DT == DT_BF16>(x);
-          }
-          const uint32_t off = (uint32_t)(row * p.ldc + col) * ES;
-          if (cvec) {
-            if constexpr (DT == DT_F32)
-              st_b128(make_uint4(h[0], h[1], h[2], h[3]), rc, n0 + col < N ? off : OOB);
-            else
-              st_b64(make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3])), rc, n0 + col < N ? off : OOB);
-          } else {
+          for (int g = 0; g < 4; ++g) {
+            const int col = wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+            float4 bc = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (MODE == 1) bc = *reinterpret_cast<const float4*>(&sbias[par][col]);
+            if constexpr (MODE == 3)
+              if (p.bias_mode == BIAS_COL) bc = *reinterpret_cast<const float4*>(&sbias[par][col]);
+            const float bb[4] = {bc.x, bc.y, bc.z, bc.w};
+            uint32_t h[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const uint32_t oe = n0 + col + e < N ? off + ES * e : OOB;
-              if constexpr (DT == DT_F32) st_b32(h[e], rc, oe);
-              else st_b16(h[e], rc, oe);
+              float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
+              if constexpr (MODE == 3) {
+                x = apply_act(p.act, x);
+                if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+              }
+              if constexpr (DT == DT_F32) h[e] = __float_as_uint(x);
+              else h[e] = st_bits<DT == DT_BF16>(x);
+            }
+            const uint32_t off = (uint32_t)(row * p.ldc + col) * ES;
+            if (MODE != 3 || cvec) {
+              if constexpr (DT == DT_F32)
+                st_b128(make_uint4(h[0], h[1], h[2], h[3]), rc, n0 + col < N ? off : OOB);
+              else
+                st_b64(make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3])), rc, n0 + col < N ? off : OOB);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t oe = n0 + col + e < N ? off + ES * e : OOB;
+                if constexpr (DT == DT_F32) st_b32(h[e], rc, oe);
+                else st_b16(h[e], rc, oe);
+              }
             }
           }
-        }
-    }
+      }
+    };
+    if (emode == 1) put(std::integral_constant<int, 1>{});
+    else if (emode == 2) put(std::integral_constant<int, 2>{});
+    else if (emode == 0) put(std::integral_constant<int, 0>{});
+    else put(std::integral_constant<int, 3>{});
     if (next >= nunits) break;
     unit = next;
   }
@@ -1317,36 +1335,57 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
     // ------------------------------------------------------------ epilogue
     // acc[i][j] holds C^T: this lane owns row wm*WM + i*32 + lane%32 and, per
     // register group g, columns wn*WN + j*32 + 8g + 4*(lane/32) + 0..3.
+    // The bias form, activation and clamp are uniform over the launch: the
+    // plain forms (no activation, no clamp; bias none / per column / per row)
+    // get straight-line code, everything else the general one.  Per-element
+    // uniform branches here cost more than the stores they guard.
+    const bool plain = p.act == WGX_ACT_NONE && !p.has_clamp;
+    const int emode = !plain ? 3 : (p.bias_mode == BIAS_COL ? 1 : (p.bias_mode == BIAS_ROW ? 2 : 0));
 #pragma unroll
     for (int q = 0; q < BM / EROWS; ++q) {
       if ((wm * WM) / EROWS == q) {
+        auto put = [&](auto mode) {
+          constexpr int MODE = decltype(mode)::value;  // 0/1/2: plain, bias none/col/row; 3: general
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const int row = wm * WM + i * 32 + frow;
-          const float rowb = p.bias_mode == BIAS_ROW ? sbias[row] : 0.0f;
+          for (int i = 0; i < TM; ++i) {
+            const int row = wm * WM + i * 32 + frow;
+            float rowb = 0.0f;
+            if constexpr (MODE == 2) rowb = sbias[row];
+            if constexpr (MODE == 3) rowb = p.bias_mode == BIAS_ROW ? sbias[row] : 0.0f;
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int col = wn * WN + j * 32 + 8 * g + 4 * fc;
-              float4 bc = make_float4(0.f, 0.f, 0.f, 0.f);
-              if (p.bias_mode == BIAS_COL) bc = *reinterpret_cast<const float4*>(&sbias[col]);
-              const float bb[4] = {bc.x, bc.y, bc.z, bc.w};
-              uint32_t h[4];
+              for (int g = 0; g < 4; ++g) {
+                const int col = wn * WN + j * 32 + 8 * g + 4 * fc;
+                float4 bc = make_float4(0.f, 0.f, 0.f, 0.f);
+                if constexpr (MODE == 1) bc = *reinterpret_cast<const float4*>(&sbias[col]);
+                if constexpr (MODE == 3)
+                  if (p.bias_mode == BIAS_COL) bc = *reinterpret_cast<const float4*>(&sbias[col]);
+                const float bb[4] = {bc.x, bc.y, bc.z, bc.w};
+                uint32_t h[4];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                float x = p.alpha * acc[i][j][4 * g + e] + rowb + bb[e];
-                x = apply_act(p.act, x);
-                if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
-                h[e] = st_bits<BF>(x);
+                for (int e = 0; e < 4; ++e) {
+                  float x = p.alpha * acc[i][j][4 * g + e];
+                  if constexpr (MODE == 1 || MODE == 3) x += bb[e];
+                  if constexpr (MODE == 2 || MODE == 3) x += rowb;
+                  if constexpr (MODE == 3) {
+                    x = apply_act(p.act, x);
+                    if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+                  }
+                  h[e] = st_bits<BF>(x);
+                }
+                *reinterpret_cast<uint2*>(stg + (row - q * EROWS) * CP + col * ES) =
+                    make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
               }
-              *reinterpret_cast<uint2*>(stg + (row - q * EROWS) * CP + col * ES) =
-                  make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-            }
-          // keep the accumulator reads of one row block together (the
-          // scheduler would otherwise hoist them all and run out of VGPRs)
-          __builtin_amdgcn_sched_barrier(0);
-        }
+            // keep the accumulator reads of one row block together (the
+            // scheduler would otherwise hoist them all and run out of VGPRs)
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        };
+        if (emode == 1) put(std::integral_constant<int, 1>{});
+        else if (emode == 2) put(std::integral_constant<int, 2>{});
+        else if (emode == 0) put(std::integral_constant<int, 0>{});
+        else put(std::integral_constant<int, 3>{});
       }
       __syncthreads();
       // EROWS rows of BN columns: 16 bytes per lane, lanes along the rows
