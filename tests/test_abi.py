@@ -135,8 +135,15 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "gemm_mfma_f16_32x64w4_conv_ws"
     monkeypatch.delenv("WGX_WS")
     assert "_kn" in conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8])
+    # batch 1: fewer register-kernel waves than two per CU, the LDS-tiled kernel
+    assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3s1_v8"
+    assert conv([1, 512, 20, 20], [512, 1, 5, 5], [1, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5s2_v4"
+    # enough planes: the register kernel (8- and 5-row bands)
+    assert conv([40, 256, 40, 40], [256, 1, 3, 3], [40, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3s1_r8v8"
+    assert conv([84, 512, 20, 20], [512, 1, 5, 5], [84, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5s2_r5v4"
+    monkeypatch.setenv("WGX_DW_KERNEL", "reg")
     assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3s1_r4v8"
-    assert conv([1, 512, 20, 20], [512, 1, 5, 5], [1, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5s2_r4v4"
+    monkeypatch.delenv("WGX_DW_KERNEL")
     # odd widths (and float32) take the LDS-tiled kernel of the same family
     assert conv([1, 6, 13, 17], [6, 1, 3, 3], [1, 6, 13, 17], pad=(1, 1), groups=6) == "depthwise_f16_3x3s1_v4"
     assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256,

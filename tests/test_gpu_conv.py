@@ -125,6 +125,61 @@ def test_depthwise_sweep(gpu_ctx, orc, pkg, dtype):
         assert_parity(got, ref, refa, dtype, k * k, f"dw {i} {dtype} {xs} k{k} s{s} {kernel}")
 
 
+def _reg_kernel_applies(iw, ow, k, s):
+    """Widths the fp16 register kernel takes: even input and output widths,
+    at most 64 segments of 4 or 8 outputs per row."""
+    ov = 4 if (ow + 3) // 4 * 4 < (ow + 7) // 8 * 8 or (s == 2 and k == 5) else 8
+    return iw % 2 == 0 and ow % 2 == 0 and (ow + ov - 1) // ov <= 64
+
+
+def test_depthwise_register_kernel_forced(gpu_ctx, orc, pkg, monkeypatch):
+    """The fp16 register kernel on every sweep shape it accepts (even widths),
+    including the small ones the automatic choice gives to the LDS-tiled
+    kernel, plain and with the SiLU + residual epilogue."""
+    W, I = pkg.wgx, pkg.inputs
+    monkeypatch.setenv("WGX_DW_KERNEL", "reg")
+    dtype = "float16"
+    for i, (xs, k, s, clamp) in enumerate(DW_SWEEP):
+        c = xs[1]
+        x = round_in(I.normal(1000 + i, xs), dtype)
+        w = round_in(I.uniform(1100 + i, (c, 1, k, k), -0.5, 0.5), dtype)
+        b = round_in(I.uniform(1200 + i, (c,), -0.5, 0.5), dtype)
+        p = (k // 2, k // 2)
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), p, groups=c)
+        cl = (-0.5, 0.75) if clamp else None
+        got, kernel = run_conv(gpu_ctx, x, w, b, dtype, (s, s), p, groups=c,
+                               out_shape=list(ref.shape), clamp=cl)
+        if cl:
+            ref = np.clip(ref, *cl)
+        if _reg_kernel_applies(xs[3], ref.shape[3], k, s):
+            assert "_r" in kernel, (xs, kernel)
+        assert_parity(got, ref, refa, dtype, k * k, f"dw reg {i} {xs} k{k} s{s} {kernel}")
+    for i, (xs, ws, s, p, d, (cs, rs), inplace) in enumerate(RESIDUAL_CASES):
+        if d != (1, 1):
+            continue
+        g = xs[1]
+        x = round_in(I.uniform(1900 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(1910 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(1920 + i, (ws[0],), -0.5, 0.5), dtype)
+        ref, refa = orc.conv2d_f64(x, w, b, s, p, d, g)
+        r = round_in(I.uniform(1930 + i, ref.shape, -2, 2), dtype)
+        tx, tw, tb = gpu_ctx.from_numpy(x, dtype), gpu_ctx.from_numpy(w, dtype), gpu_ctx.from_numpy(b, dtype)
+        tr = gpu_ctx.from_numpy(r, dtype)
+        ty = tr if inplace else gpu_ctx.tensor(dtype, list(ref.shape))
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, tb, list(s), list(p), list(d), False, [0, 0], g, ty,
+                            activation=W.ACT_SILU, residual=tr, conv_scale=cs, residual_scale=rs)
+        kernel = gpu_ctx.last_kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        if _reg_kernel_applies(xs[3], ref.shape[3], ws[2], s[1]):
+            assert "_r" in kernel, (xs, kernel)
+        want = cs * (ref / (1.0 + np.exp(-ref))) + rs * r.astype(np.float64)
+        bound = 1.1 * abs(cs) * refa + abs(rs) * np.abs(r.astype(np.float64))
+        assert_parity(ty.get_f32(), want, bound, dtype, ws[1] * ws[2] * ws[3],
+                      f"residual reg {i} {xs}x{ws} {kernel}")
+
+
 @pytest.mark.parametrize("dtype", ["float16", "float32"])
 def test_depthwise_unaligned_views(gpu_ctx, orc, pkg, dtype):
     """Input and output views that start off a 16-byte boundary (program

@@ -897,6 +897,17 @@ bool plan_fast(const DwDesc& d, DwFast& p, int& ov, int& blocks, size_t& lds) {
   return (long long)p.ppb * d.IH * d.IW < (1LL << 30);
 }
 
+int dw_device_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
 }  // namespace
 
 hipError_t launch_depthwise(const DwDesc& d, hipStream_t s, std::string* name) {
@@ -904,14 +915,27 @@ hipError_t launch_depthwise(const DwDesc& d, hipStream_t s, std::string* name) {
     DwFast f;
     int ov = 8, blocks = 0;
     size_t lds = 0;
-    // WGX_DW_KERNEL=lds|generic narrows the choice (A/B timing of the variants)
-    static const char* only = getenv("WGX_DW_KERNEL");
-    const bool allow_reg = !only, allow_lds = !only || only[0] == 'l';
+    // WGX_DW_KERNEL=reg|lds|generic narrows the choice (A/B timing of the
+    // variants, and tests of the register kernel on small shapes); a kernel
+    // that does not apply falls through to the next one
+    const char* only = getenv("WGX_DW_KERNEL");
+    const bool force_reg = only && only[0] == 'r';
+    const bool allow_reg = !only || force_reg, allow_lds = !only || force_reg || only[0] == 'l';
     DwReg rp;
     int rov = 8, R = 4;
     long long rblocks = 0;
-    if (allow_reg && plan_reg(d, rp, rov, R, rblocks)) return launch_reg_any(rp, d.KH, d.sH, rov, R, rblocks, s, name);
-    if (allow_lds && plan_fast(d, f, ov, blocks, lds)) {
+    // The register kernel runs one wave per unit: with fewer units than two
+    // per CU on small planes (batch-1 maps of at most 40 columns) the
+    // LDS-tiled kernel's 256-lane blocks fill the chip better (measured on
+    // MI355X: [1,256,40,40] 3x3 4.1 vs 4.7 us, [1,512,20,20] 5x5 s2 4.4 vs
+    // 5.6 us, [1,64,40,40] 3x3 3.9 vs 4.8 us); on large planes it loses
+    // ([1,16,160,160] 8.5 vs 5.0 us), and at batch 256 the register kernel
+    // is ahead on both configurations (107 vs 123 us, 56 vs 78 us).
+    const bool reg_ok = allow_reg && plan_reg(d, rp, rov, R, rblocks);
+    const bool fast_ok = allow_lds && plan_fast(d, f, ov, blocks, lds);
+    if (reg_ok && (force_reg || !fast_ok || d.OW > 40 || rblocks >= 2LL * dw_device_cus()))
+      return launch_reg_any(rp, d.KH, d.sH, rov, R, rblocks, s, name);
+    if (fast_ok) {
       const int K = d.KH, S = d.sH;
       if (d.dtype == WGX_FLOAT16) return launch_fast_dt<WGX_FLOAT16>(f, K, S, ov, blocks, lds, s, name);
       if (d.dtype == WGX_BFLOAT16) return launch_fast_dt<WGX_BFLOAT16>(f, K, S, ov, blocks, lds, s, name);
