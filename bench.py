@@ -183,7 +183,7 @@ def measure(W, build, n_inst_amortised, reps_shape=50, reps_amort=5):
 
 
 # ---------------------------------------------------------------- detail configs
-def detail_configs(W, I, quick=False):
+def detail_configs(W, I, quick=False, yolo=True):
     out = {}
     scale = 0.25 if quick else 1.0
 
@@ -291,7 +291,7 @@ def detail_configs(W, I, quick=False):
     rec("4_bmm_f16", k, s, a, 2.0 * 16 * 1024 * 1024 * 64, nb, "hbm", None)
 
     # config 5: the YOLO-N-style fp16 program through Node recordProgram
-    y = yolo_frame(quick)
+    y = yolo_frame(quick) if yolo else None
     if y is not None:
         out["5_yolo_n_f16"] = y
         log(f"{'5_yolo_n_f16':28s} {y['ops']} ops / {y['commands']} commands      "
@@ -332,6 +332,59 @@ def yolo_frame(quick=False):
     return res
 
 
+# ---------------------------------------------------------------- vendor libraries
+def vendor_configs():
+    """The same shapes through PyTorch-ROCm's own kernels (hipBLASLt for the
+    GEMMs, MIOpen for the convolutions), per launch, back-to-back launches
+    timed with HIP events on torch's stream (warm caches, like the at-shape
+    numbers above).  A point of comparison only: nothing of the product path
+    runs through torch."""
+    import torch
+    import torch.nn.functional as F
+
+    dev = "cuda"
+    out = {}
+
+    def t(fn, reps=100, warm=10):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps  # ms
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    M, K, N = 4096, 768, 3072
+    X = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
+    Wt = (torch.randn(N, K, device=dev, dtype=torch.float16, generator=g) * 0.02)
+    Wkn = Wt.t().contiguous()
+    b = torch.rand(N, device=dev, dtype=torch.float16, generator=g) * 0.2 - 0.1
+    out["4_addmm_f16_NN"] = t(lambda: torch.addmm(b, X, Wkn))
+    out["4_addmm_f16_NT"] = t(lambda: torch.addmm(b, X, Wt.t()))
+    A = torch.randn(16, 1024, 64, device=dev, dtype=torch.float16, generator=g)
+    B = torch.randn(16, 64, 1024, device=dev, dtype=torch.float16, generator=g)
+    out["4_bmm_f16"] = t(lambda: torch.bmm(A, B))
+    a = torch.rand(512, 512, device=dev, generator=g) * 2 - 1
+    out["1_mm_f32_512"] = t(lambda: torch.mm(a, a))
+    for dt, name in ((torch.float32, "float32"), (torch.float16, "float16")):
+        for v, c in CONV2.items():
+            x = torch.rand(c["x"], device=dev, dtype=dt, generator=g) * 2 - 1
+            w = torch.rand(c["w"], device=dev, dtype=dt, generator=g) * 0.2 - 0.1
+            bb = torch.rand(c["w"][0], device=dev, dtype=dt, generator=g) * 0.2 - 0.1
+            out[f"2{v[1]}_conv_{name}"] = t(lambda: F.conv2d(x, w, bb, stride=c["s"], padding=c["p"]), reps=50)
+    for nm, xs, ws, s_, p_ in (("3A_depthwise_f16", (1, 256, 40, 40), (256, 1, 3, 3), 1, 1),
+                               ("3B_depthwise_f16", (1, 512, 20, 20), (512, 1, 5, 5), 2, 2)):
+        x = torch.randn(xs, device=dev, dtype=torch.float16, generator=g)
+        w = torch.rand(ws, device=dev, dtype=torch.float16, generator=g) - 0.5
+        out[nm] = t(lambda: F.conv2d(x, w, None, stride=s_, padding=p_, groups=xs[1]), reps=50)
+    torch.cuda.synchronize()
+    return out
+
+
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(I, budget_s=20.0):
     """The oracle's WGSL restatement (f32, order-faithful) on this host's
@@ -370,9 +423,19 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE_SIZE runs")
+    ap.add_argument("--vendor", action="store_true",
+                    help="also time PyTorch-ROCm's hipBLASLt / MIOpen kernels on the same shapes (detail only)")
+    ap.add_argument("--no-yolo", action="store_true", help="skip the YOLO-N program (config 5) in the detail")
+    ap.add_argument("--vendor-probe", action="store_true",
+                    help=argparse.SUPPRESS)  # the child run that times the vendor kernels
     ap.add_argument("--traffic-probe", choices=list(CONV2), default=None,
                     help=argparse.SUPPRESS)  # the child run that rocprofv3 counts
     args = ap.parse_args()
+    if args.vendor_probe:
+        # torch ships its own HIP runtime: it runs in a process of its own,
+        # one that never loads libwgx
+        print(json.dumps(vendor_configs()), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on exactly one GPU (the hot path is not sharded); "
               "run with --gpus 1", file=sys.stderr)
@@ -434,7 +497,20 @@ def main():
     detail = {}
     if not args.no_detail:
         log("---- per-configuration detail (amortised = graph of instances over >= 300 MB)")
-        detail = detail_configs(W, I, quick=args.quick)
+        detail = detail_configs(W, I, quick=args.quick, yolo=not args.no_yolo)
+        if args.vendor:
+            import subprocess
+            r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-probe"],
+                               capture_output=True, text=True, timeout=600)
+            if r.returncode != 0:
+                raise RuntimeError("vendor probe failed: " + r.stderr[-2000:])
+            vendor = json.loads(r.stdout.strip().splitlines()[-1])
+            for k, ms in vendor.items():
+                if k in detail:
+                    detail[k]["vendor_ms"] = ms
+                    detail[k]["vendor_over_ours_at_shape"] = ms / detail[k]["at_shape_ms"]
+                    log(f"{k:28s} vendor library {ms*1e3:9.2f} us per launch   ours at shape "
+                        f"{detail[k]['at_shape_ms']*1e3:9.2f} us, amortised {detail[k]['amortised_ms']*1e3:9.2f} us")
         if args.detail:
             with open(args.detail, "w") as f:
                 json.dump(detail, f, indent=1)

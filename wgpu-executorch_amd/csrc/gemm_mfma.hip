@@ -1207,11 +1207,15 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   constexpr int CHB = BN * RB / 1024 / NW;              // ... B
   constexpr int DMAS = CHA + CHB;
   constexpr int CP = BN * ES + 16;                      // epilogue LDS row pitch
-  constexpr int EROWS = BM * CP <= NS * STAGE ? BM : BM / 2;  // rows per epilogue pass
+  // The whole C tile is staged at once (one epilogue pass): every instantiation
+  // has the stage memory for it.  A split into row passes for smaller stage
+  // memories gave different bits from the one-pass form in a probe at
+  // 4096 x 3072 x 768 and is not offered.
+  constexpr int EROWS = BM;  // rows per epilogue pass
   constexpr int BMAX = BM > BN ? BM : BN;
   static_assert(TM >= 1 && TN >= 1 && CHA >= 1 && CHB >= 1, "tile shape");
   static_assert(BM * RB % (1024 * NW) == 0 && BN * RB % (1024 * NW) == 0, "DMA split");
-  static_assert(EROWS * CP <= NS * STAGE && EROWS % WM == 0, "epilogue staging");
+  static_assert(EROWS * CP <= NS * STAGE, "epilogue staging: the C tile must fit the stage memory");
   static_assert((NS - 1) * DMAS < 64 && NS >= 2 && NS <= 5 && (RB == 64 || RB == 128), "stages");
 
   // 16-byte chunk c of LDS row r is stored at chunk swzc(r, c): with 64-byte
