@@ -152,7 +152,11 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     assert conv([1, 8, 12, 12], [8, 1, 3, 3], [1, 8, 12, 12], pad=(2, 2), dil=(2, 2), groups=8) == "depthwise_f16_3x3"
     assert conv([1, 8, 10, 10], [12, 4, 3, 3], [1, 12, 10, 10], pad=(1, 1), groups=2) == "conv_grouped_direct"
     assert conv([1, 2, 3, 3], [2, 2, 3, 3], [1, 2, 6, 6], (2, 2), (1, 1), transposed=True, op=(1, 1)) == "conv_transpose_direct"
-    assert conv([1, 3, 64, 64], [16, 3, 3, 3], [1, 16, 32, 32], (2, 2), (1, 1), dtype="float32").startswith("gemm_f32")
+    # a stem (K = IC*KH*KW = 27 taps, 16 output channels): the direct small-tap kernel
+    assert conv([1, 3, 64, 64], [16, 3, 3, 3], [1, 16, 32, 32], (2, 2), (1, 1), dtype="float32") == "conv_small_taps_oc16"
+    assert conv([1, 3, 64, 64], [16, 3, 3, 3], [1, 16, 32, 32], (2, 2), (1, 1)) == "conv_small_taps_oc16"
+    assert conv([1, 3, 64, 64], [48, 3, 3, 3], [1, 48, 64, 64], (1, 1), (1, 1)) == "conv_small_taps_oc64"
+    assert conv([1, 4, 64, 64], [16, 4, 3, 3], [1, 16, 64, 64], (1, 1), (1, 1)).startswith("gemm_mfma_f16")  # 36 taps
     # the reference's output-size rule, floor((I + 2p - d(K-1) - 1) / s) + 1
     with pytest.raises(E, match=r"expected output spatial \[3, 3\]"):
         conv([1, 2, 5, 5], [3, 2, 3, 3], [1, 3, 2, 2], (2, 2), (1, 1))

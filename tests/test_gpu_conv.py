@@ -214,6 +214,7 @@ def test_depthwise_unaligned_views(gpu_ctx, orc, pkg, dtype):
 SILU_CASES = [
     # x shape, w shape, stride, pad, groups -- one per kernel family
     ((1, 16, 20, 20), (32, 16, 3, 3), (1, 1), (1, 1), 1),        # implicit-im2col GEMM
+    ((1, 3, 32, 32), (16, 3, 3, 3), (2, 2), (1, 1), 1),          # small-tap direct kernel (stem)
     ((1, 32, 12, 12), (48, 32, 1, 1), (1, 1), (0, 0), 1),        # 1x1: plain GEMM
     ((1, 128, 40, 40), (256, 128, 3, 3), (2, 2), (1, 1), 1),     # split-K GEMM + reduction
     ((1, 24, 16, 16), (24, 1, 3, 3), (1, 1), (1, 1), 24),        # depthwise, register kernel (fp16)
@@ -230,7 +231,7 @@ def test_conv_silu_epilogue(gpu_ctx, orc, pkg, dtype):
     by SiLU in fp64."""
     W, I = pkg.wgx, pkg.inputs
     for i, (xs, ws, s, p, g) in enumerate(SILU_CASES):
-        d = (2, 2) if i == 5 else (1, 1)
+        d = (2, 2) if i == 6 else (1, 1)
         x = round_in(I.uniform(1800 + i, xs, -1, 1), dtype)
         w = round_in(I.uniform(1810 + i, ws, -0.5, 0.5), dtype)
         b = round_in(I.uniform(1820 + i, (ws[0],), -0.5, 0.5), dtype)
@@ -262,6 +263,9 @@ CONV_SWEEP = [
     ((1, 12, 19, 23), (12, 1, 7, 7), (2, 3), (3, 2), (1, 2), 12),    # depthwise generic
     ((1, 8, 10, 10), (12, 4, 3, 3), (1, 1), (1, 1), (1, 1), 2),      # grouped fallback
     ((1, 3, 70, 70), (8, 3, 4, 4), (3, 3), (0, 0), (1, 1), 1),       # no padding, K = 48
+    ((1, 3, 40, 36), (48, 3, 3, 3), (1, 1), (1, 1), (1, 1), 1),      # small-tap kernel, 48 of 64 channels
+    ((2, 1, 17, 19), (20, 1, 5, 5), (2, 1), (2, 1), (1, 1), 1),      # small-tap, 25 taps, batch 2, ragged
+    ((1, 2, 15, 15), (5, 2, 3, 3), (1, 2), (2, 1), (2, 2), 1),       # small-tap, dilation 2
 ]
 
 

@@ -100,6 +100,76 @@ __global__ __launch_bounds__(256) void k_direct(DcParams p) {
   stv<DT>(p.y, i, acc);
 }
 
+// Dense convolutions with few taps per output channel (IC * KH * KW <= 32,
+// OC <= OCB): the network stems, e.g. [1,3,640,640] * [16,3,3,3] s2.  As a
+// GEMM their K is too short for the matrix cores and their weight rows are
+// not 16-byte vectors (K = 27), so the GEMM path falls back to element loads
+// (28 us for that stem on MI355X).  Here one lane computes every output
+// channel of one output pixel: the weights sit in LDS as fp32 [tap][OCB]
+// (zero past OC) and are read as broadcast float4s, the lane's input window
+// is read once per tap (zero outside the image), and each output channel is
+// one coalesced store across the wave's consecutive pixels.  fp32
+// accumulation, bias first, taps in the reference's order (ic, kh, kw).
+template <int DT, int OCB>
+__global__ __launch_bounds__(256) void k_conv_small(DcParams p) {
+  constexpr int MAXT = 32;
+  __shared__ __attribute__((aligned(16))) float ws[MAXT * OCB];
+  __shared__ __attribute__((aligned(16))) float bs[OCB];
+  const int T = p.IC * p.KH * p.KW;
+  for (int i = threadIdx.x; i < MAXT * OCB; i += 256) {
+    const int t = i / OCB, oc = i - t * OCB;
+    ws[i] = (t < T && oc < p.OC) ? ldv<DT>(p.w, (long long)oc * T + t) : 0.0f;
+  }
+  for (int i = threadIdx.x; i < OCB; i += 256) bs[i] = (p.bias && i < p.OC) ? ldv<DT>(p.bias, i) : 0.0f;
+  __syncthreads();
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= p.total) return;
+  const int ow = (int)(i % p.OW);
+  const int oh = (int)((i / p.OW) % p.OH);
+  const int b = (int)(i / ((long long)p.OW * p.OH));
+  float acc[OCB];
+#pragma unroll
+  for (int oc = 0; oc < OCB; ++oc) acc[oc] = bs[oc];
+  int t = 0;
+  for (int ic = 0; ic < p.IC; ++ic)
+    for (int kh = 0; kh < p.KH; ++kh) {
+      const int ih = oh * p.sH - p.pH + kh * p.dH;
+      for (int kw = 0; kw < p.KW; ++kw, ++t) {
+        const int iw = ow * p.sW - p.pW + kw * p.dW;
+        const bool in = ih >= 0 && ih < p.IH && iw >= 0 && iw < p.IW;
+        const float xv = in ? ldv<DT>(p.x, (((long long)b * p.IC + ic) * p.IH + ih) * p.IW + iw) : 0.0f;
+        const float4* wr = reinterpret_cast<const float4*>(ws + t * OCB);
+#pragma unroll
+        for (int q = 0; q < OCB / 4; ++q) {
+          const float4 w4 = wr[q];
+          acc[4 * q] += w4.x * xv;
+          acc[4 * q + 1] += w4.y * xv;
+          acc[4 * q + 2] += w4.z * xv;
+          acc[4 * q + 3] += w4.w * xv;
+        }
+      }
+    }
+  const long long plane = (long long)p.OH * p.OW;
+  const long long ybase = (long long)b * p.OC * plane + (long long)oh * p.OW + ow;
+#pragma unroll
+  for (int oc = 0; oc < OCB; ++oc) {
+    if (oc >= p.OC) break;
+    float v = apply_act(p.act, acc[oc]);
+    if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
+    stv<DT>(p.y, ybase + oc * plane, v);
+  }
+}
+
+template <int DT>
+hipError_t go_small(const DcParams& p, int ocb, hipStream_t s) {
+  if (is_dry(s) || p.total == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((p.total + 255) / 256);
+  if (ocb == 16) hipLaunchKernelGGL((k_conv_small<DT, 16>), dim3(blocks), dim3(256), 0, s, p);
+  else if (ocb == 32) hipLaunchKernelGGL((k_conv_small<DT, 32>), dim3(blocks), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((k_conv_small<DT, 64>), dim3(blocks), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
 template <int DT>
 hipError_t go(const DcParams& p, bool transposed, hipStream_t s) {
   if (is_dry(s) || p.total == 0) return hipSuccess;
@@ -112,6 +182,10 @@ hipError_t go(const DcParams& p, bool transposed, hipStream_t s) {
 }
 
 }  // namespace
+
+bool small_tap_conv(const DirectConvDesc& d) {
+  return !d.transposed && d.groups == 1 && d.IC * d.KH * d.KW <= 32 && d.OC <= 64;
+}
 
 hipError_t launch_direct_conv(const DirectConvDesc& d, hipStream_t s, std::string* name) {
   DcParams p;
@@ -139,6 +213,15 @@ hipError_t launch_direct_conv(const DirectConvDesc& d, hipStream_t s, std::strin
   p.act = d.act;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
+  if (small_tap_conv(d)) {
+    p.total = (long long)d.B * d.OH * d.OW;
+    const int ocb = d.OC <= 16 ? 16 : (d.OC <= 32 ? 32 : 64);
+    if (name) *name = "conv_small_taps_oc" + std::to_string(ocb);
+    if (p.total >= (1LL << 31) * 256LL) return hipErrorInvalidValue;
+    if (d.dtype == WGX_FLOAT16) return go_small<WGX_FLOAT16>(p, ocb, s);
+    if (d.dtype == WGX_BFLOAT16) return go_small<WGX_BFLOAT16>(p, ocb, s);
+    return go_small<WGX_FLOAT32>(p, ocb, s);
+  }
   p.total = (long long)d.B * d.OC * d.OH * d.OW;
   if (name) *name = d.transposed ? "conv_transpose_direct" : "conv_grouped_direct";
   if (d.dtype == WGX_FLOAT16) return go<WGX_FLOAT16>(p, d.transposed, s);

@@ -116,6 +116,9 @@ struct DirectConvDesc {
   float cmin, cmax;
 };
 hipError_t launch_direct_conv(const DirectConvDesc& d, hipStream_t s, std::string* name);
+// Dense convolutions with at most 32 taps per output channel and at most 64
+// output channels: launch_direct_conv runs them on its small-tap kernel.
+bool small_tap_conv(const DirectConvDesc& d);
 
 // Elementwise family (eltwise.hip).
 struct BcastDesc {

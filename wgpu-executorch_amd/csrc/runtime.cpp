@@ -613,7 +613,10 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
     return c->fail(WGX_ERR_INVALID, "convolution: a residual is supported on depthwise convolutions only");
   const ConvGeom geom{(int)IH, (int)IW, (int)OW, sH, sW, pH, pW, (int)KH, (int)KW, dH, dW};
   const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0;
-  const bool gemm_ok = !args->transposed && groups == 1 &&
+  // a few taps per output channel (network stems, K = IC*KH*KW <= 32): the
+  // direct small-tap kernel, not a GEMM with a 1-2 step K loop
+  const bool small_taps = !args->transposed && groups == 1 && !pointwise && IC * KH * KW <= 32 && OC <= 64;
+  const bool gemm_ok = !args->transposed && groups == 1 && !small_taps &&
                        (pointwise || conv_ktab_fits((int)(IC * KH * KW), (int)IC, geom));
   if (gemm_ok) {
     GemmDesc d{};
