@@ -100,6 +100,45 @@ def traffic_probe(W, I, v):
         ctx.destroy()
 
 
+# One configuration, recorded once and submitted PROBE_REPS times without a
+# graph (one dispatch per launch): the child run that rocprofv3 --pmc counts.
+KERNEL_PROBES = ("conv2a_f32", "conv2b_f32", "conv2a_f16", "addmm_nt", "addmm_nn", "bmm",
+                 "dw3a", "dw3b", "dw3a_b256", "dw3b_b256")
+
+
+def kernel_probe(W, I, name):
+    ctx = W.Context(0)
+    try:
+        if name.startswith("conv"):
+            build_conv(ctx, I, CONV2[name[4:6]], "float32" if name.endswith("f32") else "float16", 40)
+        elif name.startswith("addmm"):
+            M, K, N = 4096, 768, 3072
+            nt = name.endswith("nt")
+            x = ctx.from_numpy(I.normal(1, (M, K)), "float16")
+            w = ctx.from_numpy(I.normal(2, (N, K) if nt else (K, N), 0, 0.02), "float16")
+            b = ctx.from_numpy(I.uniform(3, (N,), -0.1, 0.1), "float16")
+            ctx.addmm(b, x, w, ctx.tensor("float16", [M, N]), trans_b=nt)
+        elif name == "bmm":
+            a = ctx.from_numpy(I.normal(1, (16, 1024, 64)), "float16")
+            bb = ctx.from_numpy(I.normal(2, (16, 64, 1024)), "float16")
+            ctx.bmm(a, bb, ctx.tensor("float16", [16, 1024, 1024]))
+        else:
+            batch = 256 if name.endswith("b256") else 1
+            C, H, K, S = (256, 40, 3, 1) if name.startswith("dw3a") else (512, 20, 5, 2)
+            OH = (H + 2 * (K // 2) - K) // S + 1
+            x = ctx.from_numpy(I.normal(3, (batch, C, H, H)), "float16")
+            w = ctx.from_numpy(I.uniform(4, (C, 1, K, K), -0.5, 0.5), "float16")
+            ctx.convolution(x, w, None, [S, S], [K // 2, K // 2], [1, 1], False, [0, 0], C,
+                            ctx.tensor("float16", [batch, C, OH, OH]))
+        print(name, ctx.last_kernel, flush=True)
+        ctx.set_graph_mode(False)
+        for _ in range(PROBE_REPS):
+            ctx.submit()
+        ctx.sync()
+    finally:
+        ctx.destroy()
+
+
 def measure_traffic(v):
     """HBM bytes per step of the headline conv `v` (its GEMM dispatch plus the
     split-K reduction when there is one) from two rocprofv3 --pmc runs
@@ -426,6 +465,8 @@ def main():
     ap.add_argument("--vendor", action="store_true",
                     help="also time PyTorch-ROCm's hipBLASLt / MIOpen kernels on the same shapes (detail only)")
     ap.add_argument("--no-yolo", action="store_true", help="skip the YOLO-N program (config 5) in the detail")
+    ap.add_argument("--kernel-probe", choices=KERNEL_PROBES, default=None,
+                    help="record one configuration and submit it a few times (for rocprofv3 --pmc runs)")
     ap.add_argument("--vendor-probe", action="store_true",
                     help=argparse.SUPPRESS)  # the child run that times the vendor kernels
     ap.add_argument("--traffic-probe", choices=list(CONV2), default=None,
@@ -447,6 +488,9 @@ def main():
     W, I = pkg.wgx, pkg.inputs
     if args.traffic_probe:
         traffic_probe(W, I, args.traffic_probe)
+        return
+    if args.kernel_probe:
+        kernel_probe(W, I, args.kernel_probe)
         return
 
     # ---- headline: config 2 (2a + 2b), float32, one submit per step

@@ -153,10 +153,11 @@ __global__ __launch_bounds__(256) void k_conv_small(DcParams p) {
   const long long ybase = (long long)b * p.OC * plane + (long long)oh * p.OW + ow;
 #pragma unroll
   for (int oc = 0; oc < OCB; ++oc) {
-    if (oc >= p.OC) break;
-    float v = apply_act(p.act, acc[oc]);
-    if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
-    stv<DT>(p.y, ybase + oc * plane, v);
+    if (oc < p.OC) {
+      float v = apply_act(p.act, acc[oc]);
+      if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
+      stv<DT>(p.y, ybase + oc * plane, v);
+    }
   }
 }
 
