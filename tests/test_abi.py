@@ -134,7 +134,10 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     monkeypatch.setenv("WGX_WS", "1x2w4")
     assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "gemm_mfma_f16_32x64w4_conv_ws"
     monkeypatch.delenv("WGX_WS")
-    assert "_kn" in conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8])
+    # 1x1: a plain GEMM over the [IC, H*W] plane when its 64 x 64 tiles fill the CUs,
+    # else the one-tap im2col form on the wave-split kernel
+    assert conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8]).endswith("_conv_ws")
+    assert "_kn" in conv([1, 16, 160, 160], [32, 16, 1, 1], [1, 32, 160, 160])
     # batch 1: fewer register-kernel waves than two per CU, the LDS-tiled kernel
     assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3s1_v8"
     assert conv([1, 512, 20, 20], [512, 1, 5, 5], [1, 512, 10, 10], (2, 2), (2, 2), groups=512) == "depthwise_f16_5x5s2_v4"

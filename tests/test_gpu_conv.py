@@ -215,7 +215,8 @@ SILU_CASES = [
     # x shape, w shape, stride, pad, groups -- one per kernel family
     ((1, 16, 20, 20), (32, 16, 3, 3), (1, 1), (1, 1), 1),        # implicit-im2col GEMM
     ((1, 3, 32, 32), (16, 3, 3, 3), (2, 2), (1, 1), 1),          # small-tap direct kernel (stem)
-    ((1, 32, 12, 12), (48, 32, 1, 1), (1, 1), (0, 0), 1),        # 1x1: plain GEMM
+    ((1, 32, 12, 12), (48, 32, 1, 1), (1, 1), (0, 0), 1),        # 1x1, few tiles: one-tap im2col
+    ((1, 16, 160, 160), (32, 16, 1, 1), (1, 1), (0, 0), 1),      # 1x1, many tiles: plain GEMM
     ((1, 128, 40, 40), (256, 128, 3, 3), (2, 2), (1, 1), 1),     # split-K GEMM + reduction
     ((1, 24, 16, 16), (24, 1, 3, 3), (1, 1), (1, 1), 24),        # depthwise, register kernel (fp16)
     ((1, 6, 13, 17), (6, 1, 5, 5), (2, 2), (2, 2), 6),           # depthwise, LDS kernel
@@ -231,7 +232,7 @@ def test_conv_silu_epilogue(gpu_ctx, orc, pkg, dtype):
     by SiLU in fp64."""
     W, I = pkg.wgx, pkg.inputs
     for i, (xs, ws, s, p, g) in enumerate(SILU_CASES):
-        d = (2, 2) if i == 6 else (1, 1)
+        d = (2, 2) if i == 7 else (1, 1)
         x = round_in(I.uniform(1800 + i, xs, -1, 1), dtype)
         w = round_in(I.uniform(1810 + i, ws, -0.5, 0.5), dtype)
         b = round_in(I.uniform(1820 + i, (ws[0],), -0.5, 0.5), dtype)
@@ -252,7 +253,8 @@ def test_conv_silu_epilogue(gpu_ctx, orc, pkg, dtype):
 CONV_SWEEP = [
     # x shape, w shape, stride, pad, dilation, groups
     ((1, 3, 64, 64), (16, 3, 3, 3), (2, 2), (1, 1), (1, 1), 1),      # stem: K = 27
-    ((1, 32, 20, 20), (64, 32, 1, 1), (1, 1), (0, 0), (1, 1), 1),    # pointwise
+    ((1, 32, 20, 20), (64, 32, 1, 1), (1, 1), (0, 0), (1, 1), 1),    # pointwise, few tiles: one-tap im2col
+    ((1, 16, 160, 160), (32, 16, 1, 1), (1, 1), (0, 0), (1, 1), 1),  # pointwise, 400 tiles: [IC, H*W] GEMM
     ((2, 32, 17, 19), (48, 32, 1, 1), (1, 1), (0, 0), (1, 1), 1),    # pointwise, batch 2, ragged
     ((1, 16, 21, 13), (24, 16, 1, 1), (2, 2), (0, 0), (1, 1), 1),    # strided 1x1 -> im2col path
     ((2, 24, 15, 15), (40, 24, 3, 3), (1, 1), (2, 2), (2, 2), 1),    # dilation 2

@@ -385,6 +385,16 @@ static bool f32_on_mfma() {
   return v == 1;
 }
 
+// Compute units of the context's device (256 on MI355X; host-only contexts
+// assume that).
+static int device_cu_count(wgx_ctx* c) {
+  int cus = 0;
+  if (!c->d->has_dev ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->d->device) != hipSuccess || cus <= 0)
+    cus = 256;
+  return cus;
+}
+
 static int record_gemm(wgx_ctx* c, GemmDesc d) {
   std::string name;
   bool mfma = d.dtype != WGX_FLOAT32;
@@ -612,7 +622,15 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
   if (res)
     return c->fail(WGX_ERR_INVALID, "convolution: a residual is supported on depthwise convolutions only");
   const ConvGeom geom{(int)IH, (int)IW, (int)OW, sH, sW, pH, pW, (int)KH, (int)KW, dH, dW};
-  const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0;
+  // A 1x1 convolution is a plain GEMM with the input plane as its [IC, H*W]
+  // operand -- unless it has fewer 64 x 64 output tiles than CUs: then it
+  // goes through the im2col form (a one-tap table) to the wave-split kernel,
+  // which splits K over the waves of each tile (measured on the YOLO-N 640
+  // frame, whose 1x1 convolutions at 80x80 and below have 28-200 tiles:
+  // 527 -> 481 us).
+  const long long pw_tiles = (OC + 63) / 64 * ((OH * OW + 63) / 64) * B;
+  const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0 &&
+                         pw_tiles >= device_cu_count(c);
   // a few taps per output channel (network stems, K = IC*KH*KW <= 32): the
   // direct small-tap kernel, not a GEMM with a 1-2 step K loop
   const bool small_taps = !args->transposed && groups == 1 && !pointwise && IC * KH * KW <= 32 && OC <= 64;
