@@ -66,6 +66,49 @@ def test_graph_replays_match_eager(pkg, orc):
     assert np.array_equal(results[True].view(np.uint16), results[False].view(np.uint16))
 
 
+def test_graph_keeps_buffer_order(pkg):
+    """A captured graph of independent and dependent commands (two unrelated
+    convolutions and an mm, an add joining two of them, a read after write
+    through a copy, an overwrite of an input an earlier command read): each
+    replay equals the eager sequence bit for bit, replay after replay."""
+    W, I = pkg.wgx, pkg.inputs
+    results = {}
+    for graph in (False, True):
+        ctx = W.Context(0)
+        try:
+            ctx.set_graph_mode(graph)
+            xa = ctx.from_numpy(I.as_f16(I.uniform(1, (1, 32, 40, 40), -1, 1)), "float16")
+            wa = ctx.from_numpy(I.as_f16(I.kaiming_uniform(2, (64, 32, 3, 3))), "float16")
+            xb = ctx.from_numpy(I.as_f16(I.uniform(3, (1, 64, 40, 40), -1, 1)), "float16")
+            wb = ctx.from_numpy(I.as_f16(I.kaiming_uniform(4, (64, 64, 1, 1))), "float16")
+            ma = ctx.from_numpy(I.as_f16(I.uniform(5, (512, 256), -1, 1)), "float16")
+            mb = ctx.from_numpy(I.as_f16(I.uniform(6, (256, 384), -1, 1)), "float16")
+            xnew = ctx.from_numpy(I.as_f16(I.uniform(7, (1, 32, 40, 40), -1, 1)), "float16")
+            wz = ctx.from_numpy(I.as_f16(I.uniform(8, (64, 1, 3, 3), -0.5, 0.5)), "float16")
+            ya, yb, s_, z, yz = (ctx.tensor("float16", [1, 64, 40, 40]) for _ in range(5))
+            yc = ctx.tensor("float16", [512, 384])
+            ctx.convolution(xa, wa, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 1, ya)
+            ctx.convolution(xb, wb, None, [1, 1], [0, 0], [1, 1], False, [0, 0], 1, yb)   # independent
+            ctx.mm(ma, mb, yc)                                                            # independent
+            ctx.add(ya, yb, s_)                                                           # joins both
+            ctx.copy(s_, z)                                                               # read after write
+            ctx.convolution(z, wz, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 64, yz)
+            ctx.copy(xnew, xa)                                   # overwrites an input the first conv read
+            outs = []
+            for rep in range(3):
+                ctx.submit()
+                ctx.sync()
+                outs.append([t.get_data().copy() for t in (ya, yb, yc, s_, z, yz, xa)])
+            results[graph] = outs
+        finally:
+            ctx.destroy()
+    for rep, (e, g) in enumerate(zip(results[False], results[True])):
+        for k, (a, b) in enumerate(zip(e, g)):
+            assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"replay {rep} tensor {k}"
+    # the second replay's first conv read the overwritten input
+    assert not np.array_equal(results[True][0][0].view(np.uint16), results[True][1][0].view(np.uint16))
+
+
 def test_time_submits_positive(pkg):
     W, I = pkg.wgx, pkg.inputs
     ctx = W.Context(0)
