@@ -176,6 +176,11 @@ def test_js_host_records_the_program(Y, tmp_path):
     assert base - res[("--no-views",)]["commands"] == 2 * n + adds
     assert base - res[("--no-fuse",)]["commands"] == v
     assert base - res[()]["commands"] == 2 * n + adds + v
+    # the caller's input and output tensors bound in place: two copies fewer
+    cmd = [NODE, RUNNER, str(tmp_path), "--device", "-1", "--record-only", "--no-bind-io"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert json.loads(r.stdout.strip().splitlines()[-1])["commands"] == res[()]["commands"] + 2
 
 
 # ------------------------------------------------------------ evaluator pins
@@ -285,8 +290,9 @@ def test_yolo_program_gpu_matches_cpu_160(Y, orc, tmp_path):
 
 @needs_node
 @pytest.mark.gpu
-@pytest.mark.parametrize("flags", [("--no-fuse",), ("--no-views",), ("--no-fuse", "--no-views")],
-                         ids=["views", "fused", "op_by_op"])
+@pytest.mark.parametrize("flags", [("--no-fuse",), ("--no-views",), ("--no-fuse", "--no-views"),
+                                   ("--no-bind-io",)],
+                         ids=["views", "fused", "op_by_op", "copied_io"])
 def test_yolo_program_gpu_matches_cpu_160_variants(Y, orc, tmp_path, flags):
     _gpu_vs_cpu(Y, tmp_path, 160, flags)
 

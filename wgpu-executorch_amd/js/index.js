@@ -313,6 +313,47 @@ class WgpuExecutionContext {
       tensors.set(i, this.tensor(v.dtype, v.shape, buffer));
     });
 
+    // Program inputs and outputs bound to the caller's tensors (no copy in or
+    // out; this build's own pass, switched off with {bindIO: false}): an input
+    // that no op writes is read in place; an output that exactly one op
+    // writes is written in place by that op.  Each bound tensor must have the
+    // value's dtype and size, and the caller's inputs and outputs must not
+    // share memory.  The copies' semantics hold: the chain reads the caller's
+    // input as it is at submit time, and nothing else writes the output.
+    const bound = new Set();
+    if (!(options && options.bindIO === false)) {
+      const writers = new Map();
+      for (const op of program.chain) {
+        const outs = opOutputs(op, program.values);
+        if (op.name === 'aten.max_pool2d_with_indices.default' && op.args.length >= 2) {
+          outs.push(op.args[op.args.length - 2]);  // values and indices are both written
+        }
+        for (const id of outs) writers.set(id, (writers.get(id) || 0) + 1);
+      }
+      const ins = args.slice(0, numInputs), outs = args.slice(numInputs);
+      const ioClash = ins.some((a) => a instanceof Tensor && outs.some((o) => o instanceof Tensor && overlaps(a, o)));
+      const fits = (t, id) => t instanceof Tensor && t.dtype === program.values[id].dtype &&
+        t.byteLength === valueBytes(program.values[id]);
+      const once = (ids) => (id) => ids.filter((x) => x === id).length === 1;
+      const inOnce = once(program.inputIds), outOnce = once(program.outputIds);
+      if (!ioClash) {
+        program.inputIds.forEach((id, i) => {
+          if (fits(ins[i], id) && inOnce(id) && !writers.has(id) && !program.outputIds.includes(id) &&
+              !views.place.has(id)) {
+            tensors.set(id, ins[i]);
+            bound.add(id);
+          }
+        });
+        program.outputIds.forEach((id, i) => {
+          if (fits(outs[i], id) && outOnce(id) && writers.get(id) === 1 && !program.inputIds.includes(id) &&
+              !views.place.has(id) && !constOffset.has(id)) {
+            tensors.set(id, outs[i]);
+            bound.add(id);
+          }
+        });
+      }
+    }
+
     // weights: one staging image of the constant slab, one upload
     if (constSlab) {
       const staging = new Uint8Array(constBytes);
@@ -373,6 +414,7 @@ class WgpuExecutionContext {
       const dst = tensors.get(program.inputIds[i]);
       if (!(src instanceof Tensor)) continue;
       if (dst === undefined) throw new Error(`program: no tensor for input value ${program.inputIds[i]}`);
+      if (bound.has(program.inputIds[i])) continue;  // the chain reads the caller's tensor itself
       this.copy(src, dst);
     }
 
@@ -395,6 +437,7 @@ class WgpuExecutionContext {
       const dst = args[numInputs + i];
       if (!(dst instanceof Tensor)) throw new Error(`program: output ${i} must be a Tensor`);
       if (src === undefined) throw new Error(`program: no tensor for output value ${program.outputIds[i]}`);
+      if (bound.has(program.outputIds[i])) continue;  // its producer wrote the caller's tensor
       this.copy(src, dst);
     }
     return this;

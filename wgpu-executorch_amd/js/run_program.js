@@ -16,6 +16,8 @@
  * --record-only validates and records the program without running it (it
  * works on the host-only device -1).  --no-fuse records no conv -> sigmoid ->
  * mul folding, --no-views runs every cat / split / view_copy as a copy,
+ * --no-bind-io copies the input into and the output out of the memory plan
+ * instead of binding the caller's tensors,
  * --eager replays the recorded launches one by one on the stream instead of
  * through a HIP graph.
  */
@@ -24,7 +26,8 @@ const path = require('path');
 const W = require('./index.js');
 
 function parseArgs(argv) {
-  const a = { dir: null, device: 0, warmup: 5, reps: 50, out: null, recordOnly: false, fuse: true, views: true, eager: false };
+  const a = { dir: null, device: 0, warmup: 5, reps: 50, out: null, recordOnly: false, fuse: true, views: true,
+    bindIO: true, eager: false };
   for (let i = 0; i < argv.length; i++) {
     const k = argv[i];
     if (k === '--device') a.device = Number(argv[++i]);
@@ -34,6 +37,7 @@ function parseArgs(argv) {
     else if (k === '--record-only') a.recordOnly = true;
     else if (k === '--no-fuse') a.fuse = false;
     else if (k === '--no-views') a.views = false;
+    else if (k === '--no-bind-io') a.bindIO = false;
     else if (k === '--eager') a.eager = true;
     else a.dir = k;
   }
@@ -58,7 +62,7 @@ async function main() {
 
   if (args.eager) ctx.setGraphMode(false);
   const t0 = process.hrtime.bigint();
-  ctx.recordProgram(program, weights, [input, output], { fuse: args.fuse, views: args.views });
+  ctx.recordProgram(program, weights, [input, output], { fuse: args.fuse, views: args.views, bindIO: args.bindIO });
   const recordMs = Number(process.hrtime.bigint() - t0) / 1e6;
   if (args.recordOnly) {
     console.log(JSON.stringify({ record_ms: recordMs, commands: ctx.commandCount, ops: program.chain.length }));
