@@ -137,6 +137,9 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     # 1x1: a plain GEMM over the [IC, H*W] plane when its 64 x 64 tiles fill the CUs,
     # else the one-tap im2col form on the wave-split kernel
     assert conv([1, 64, 8, 8], [64, 64, 1, 1], [1, 64, 8, 8]).endswith("_conv_ws")
+    # one K slice of 64 channels: the 4-wave form (8 waves would leave 7 without a slice)
+    assert conv([1, 64, 40, 40], [64, 64, 1, 1], [1, 64, 40, 40]) == "gemm_mfma_f16_32x32w4_conv_ws"
+    assert conv([1, 512, 20, 20], [64, 512, 1, 1], [1, 64, 20, 20]) == "gemm_mfma_f16_32x32w8_conv_ws"
     assert "_kn" in conv([1, 16, 160, 160], [32, 16, 1, 1], [1, 32, 160, 160])
     # batch 1: fewer register-kernel waves than two per CU, the LDS-tiled kernel
     assert conv([1, 256, 40, 40], [256, 1, 3, 3], [1, 256, 40, 40], pad=(1, 1), groups=256) == "depthwise_f16_3x3s1_v8"

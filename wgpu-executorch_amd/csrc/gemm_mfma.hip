@@ -2282,6 +2282,10 @@ bool ws_choice(const GemmDesc& d, const Plan& pl, WsCfg* cfg) {
   if (tiles32 <= cus) *cfg = WsCfg{1, 1, 8};
   else if (pl.f32) *cfg = WsCfg{2, 1, 4};
   else *cfg = tiles2 <= cus ? WsCfg{2, 1, 8} : WsCfg{2, 1, 4};
+  // fewer K slices than waves (1x1 convolutions over few channels): the
+  // 4-wave form of the same tile, the others would have no slice at all
+  const int kt = (d.K + 128 / pl.es - 1) / (128 / pl.es);
+  if (cfg->w == 8 && kt < 8 && !getenv_is0("WGX_WS_FEW_K")) cfg->w = 4;
   return fits(*cfg);
 }
 
