@@ -2283,9 +2283,14 @@ bool ws_choice(const GemmDesc& d, const Plan& pl, WsCfg* cfg) {
   else if (pl.f32) *cfg = WsCfg{2, 1, 4};
   else *cfg = tiles2 <= cus ? WsCfg{2, 1, 8} : WsCfg{2, 1, 4};
   // fewer K slices than waves (1x1 convolutions over few channels): the
-  // 4-wave form of the same tile, the others would have no slice at all
+  // 4-wave form of the same tile, the others would have no slice at all.
+  // WGX_WS_FEW_K=n moves the threshold (0: always 8 waves).
   const int kt = (d.K + 128 / pl.es - 1) / (128 / pl.es);
-  if (cfg->w == 8 && kt < 8 && !getenv_is0("WGX_WS_FEW_K")) cfg->w = 4;
+  static const int few_k = [] {
+    const char* v = getenv("WGX_WS_FEW_K");
+    return v ? atoi(v) : 8;
+  }();
+  if (cfg->w == 8 && kt < few_k) cfg->w = 4;
   return fits(*cfg);
 }
 
