@@ -160,6 +160,53 @@ def test_elementwise_ops(pkg, orc):
         ctx.destroy()
 
 
+def _np_maxpool_same(a, k):
+    p = k // 2
+    pad = np.pad(a.astype(np.float64), ((0, 0), (0, 0), (p, p), (p, p)), constant_values=-np.inf)
+    H, W = a.shape[2], a.shape[3]
+    return np.max(np.stack([pad[:, :, i:i + H, j:j + W] for i in range(k) for j in range(k)]), 0)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_chained_max_pools_fold(pkg, dtype):
+    """Consecutive same-size max-pools, each pooling the previous output (the
+    SPPF block), fold into one launch that writes every output; the results
+    equal pooling step by step.  A pool whose input is not the previous
+    output, or whose output overlaps the chain's input, stays separate."""
+    W, I = pkg.wgx, pkg.inputs
+    ctx = W.Context(0)
+    try:
+        a = I.uniform(40, (2, 8, 13, 17), -3, 3).astype(np.float16 if dtype == "float16" else np.float32)
+        x = ctx.from_numpy(a, dtype)
+        ys = [ctx.tensor(dtype, [2, 8, 13, 17]) for _ in range(4)]
+        args = ([5, 5], [1, 1], [2, 2], [1, 1])
+        ctx.max_pool2d(x, *args, ys[0])
+        ctx.max_pool2d(ys[0], *args, ys[1])
+        assert ctx.last_kernel == "max_pool2d_chain2"
+        ctx.max_pool2d(ys[1], *args, ys[2])
+        assert ctx.last_kernel == "max_pool2d_chain3"
+        n_cmds = ctx.command_count
+        ctx.max_pool2d(ys[2], *args, ys[3])  # a fourth does not join (at most 3)
+        assert ctx.command_count == n_cmds + 1
+        ctx.submit()
+        ctx.sync()
+        want = a.astype(np.float64)
+        for y in ys:
+            want = _np_maxpool_same(want, 5)
+            np.testing.assert_array_equal(y.get_f32(), want.astype(np.float32))
+        # no fold: the second pool reads the chain's input, not its output
+        ctx.reset()
+        z = [ctx.tensor(dtype, [2, 8, 13, 17]) for _ in range(2)]
+        ctx.max_pool2d(x, *args, z[0])
+        ctx.max_pool2d(x, [3, 3], [1, 1], [1, 1], [1, 1], z[1])
+        assert ctx.command_count == 2
+        ctx.submit()
+        ctx.sync()
+        np.testing.assert_array_equal(z[1].get_f32(), _np_maxpool_same(a, 3).astype(np.float32))
+    finally:
+        ctx.destroy()
+
+
 def test_shared_contexts_order_and_freed_buffers(pkg):
     """Two contexts over one device share its queue: work submitted from one
     is visible to the other's later submit without a sync in between.  A

@@ -115,7 +115,78 @@ __global__ __launch_bounds__(256) void k_maxpool(int BC, int IH, int IW, int OH,
   stv<DT>(y, i, m);
 }
 
+// A chain of n (2 or 3) max-pools of one K x K window, stride 1, padding
+// P = K/2, dilation 1, each pooling the previous one's output: pooling a
+// pooled map again is a pool of the larger window 2K-1 (then 3K-2) over the
+// first input, the borders padded with -inf either way.  One block per plane:
+// the plane with a -inf border of R = nP in LDS, row maxima of radius P, 2P
+// and 3P (clipped to R), then column maxima of the same radii: output k is
+// the Chebyshev window of radius kP.
+template <int DT>
+__global__ __launch_bounds__(256) void k_maxpool_chain(int H, int W, int P, int n, const void* x, void* y1,
+                                                       void* y2, void* y3) {
+  extern __shared__ float sm[];
+  const int R = n * P, PH = H + 2 * R, PW = W + 2 * R;
+  float* xs = sm;             // [PH][PW]
+  float* hr = sm + PH * PW;   // [3][PH][W]
+  const long long plane = blockIdx.x;
+  const long long base = plane * H * W;
+  for (int i = threadIdx.x; i < PH * PW; i += 256) {
+    const int r = i / PW - R, c = i % PW - R;
+    xs[i] = (r >= 0 && r < H && c >= 0 && c < W) ? ldv<DT>(x, base + (long long)r * W + c) : -INFINITY;
+  }
+  __syncthreads();
+  const int r1 = P, r2 = min(2 * P, R), r3 = min(3 * P, R);
+  for (int i = threadIdx.x; i < PH * W; i += 256) {
+    const int r = i / W, c = i % W;
+    const float* row = xs + r * PW + c + R;
+    float m1 = -INFINITY, m2 = -INFINITY, m3 = -INFINITY;
+    for (int d = -r3; d <= r3; ++d) {
+      const float v = row[d];
+      const int ad = d < 0 ? -d : d;
+      m3 = fmaxf(m3, v);
+      if (ad <= r2) m2 = fmaxf(m2, v);
+      if (ad <= r1) m1 = fmaxf(m1, v);
+    }
+    hr[i] = m1;
+    hr[PH * W + i] = m2;
+    hr[2 * PH * W + i] = m3;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < H * W; i += 256) {
+    const int oh = i / W, ow = i % W;
+    const float* c0 = hr + (oh + R) * W + ow;
+    float a1 = -INFINITY, a2 = -INFINITY, a3 = -INFINITY;
+    for (int d = -r1; d <= r1; ++d) a1 = fmaxf(a1, c0[d * W]);
+    for (int d = -r2; d <= r2; ++d) a2 = fmaxf(a2, c0[PH * W + d * W]);
+    for (int d = -r3; d <= r3; ++d) a3 = fmaxf(a3, c0[2 * PH * W + d * W]);
+    stv<DT>(y1, base + i, a1);
+    stv<DT>(y2, base + i, a2);
+    if (n == 3) stv<DT>(y3, base + i, a3);
+  }
+}
+
 }  // namespace
+
+size_t max_pool_chain_lds(int H, int W, int P, int n) {
+  const long long R = (long long)n * P, PH = H + 2 * R, PW = W + 2 * R;
+  return (size_t)(PH * PW + 3 * PH * W) * sizeof(float);
+}
+
+hipError_t launch_max_pool_chain(int dtype, int BC, int H, int W, int P, int n, const void* x, void* y1, void* y2,
+                                 void* y3, hipStream_t s, std::string* name) {
+  if (name) *name = n == 2 ? "max_pool2d_chain2" : "max_pool2d_chain3";
+  const size_t lds = max_pool_chain_lds(H, W, P, n);
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  if (BC == 0 || is_dry(s)) return hipSuccess;
+  if (dtype == WGX_FLOAT16)
+    hipLaunchKernelGGL(k_maxpool_chain<WGX_FLOAT16>, dim3(BC), dim3(256), lds, s, H, W, P, n, x, y1, y2, y3);
+  else if (dtype == WGX_BFLOAT16)
+    hipLaunchKernelGGL(k_maxpool_chain<WGX_BFLOAT16>, dim3(BC), dim3(256), lds, s, H, W, P, n, x, y1, y2, y3);
+  else
+    hipLaunchKernelGGL(k_maxpool_chain<WGX_FLOAT32>, dim3(BC), dim3(256), lds, s, H, W, P, n, x, y1, y2, y3);
+  return hipGetLastError();
+}
 
 hipError_t launch_binary(const BcastDesc& d, hipStream_t s, std::string* name) {
   if (name) *name = d.op == 0 ? "binary_add" : "binary_mul";

@@ -145,6 +145,12 @@ hipError_t launch_slab_copy(int elsize, long long outer, long long inner_src,
                             std::string* name);
 hipError_t launch_upsample_nearest(int dtype, int BC, int IH, int IW, int OH, int OW,
                                    const void* x, void* y, hipStream_t s, std::string* name);
+// n = 2 or 3 chained K x K max-pools (stride 1, padding P = K/2, dilation 1)
+// of one [BC, H, W] map in one pass: y1 = pool(x), y2 = pool(y1), y3 = pool(y2).
+// One block per plane, max_pool_chain_lds bytes of LDS (at most 64 KB).
+size_t max_pool_chain_lds(int H, int W, int P, int n);
+hipError_t launch_max_pool_chain(int dtype, int BC, int H, int W, int P, int n, const void* x, void* y1, void* y2,
+                                 void* y3, hipStream_t s, std::string* name);
 hipError_t launch_max_pool(int dtype, int BC, int IH, int IW, int OH, int OW, int KH, int KW,
                            int sH, int sW, int pH, int pW, int dH, int dW, const void* x,
                            void* y, hipStream_t s, std::string* name);

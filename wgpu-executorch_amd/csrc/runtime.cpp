@@ -119,6 +119,15 @@ struct wgx_ctx {
   int graph_mode = 1;
   std::string err;
   std::string last_kernel;
+  // the last command, when it is a mergeable max-pool (or a chain of them):
+  // stride 1, padding K/2 ("same" size), dilation 1, square odd window
+  struct PoolChain {
+    int cmd = -1;  // index in cmds
+    int dt, BC, H, W, P, n;
+    const void* x;
+    void* y[3];
+    size_t bytes;  // of x and of every output
+  } pool;
 
   int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -922,10 +931,55 @@ int wgx_record_max_pool2d(wgx_ctx* c, const wgx_tensor* in, const int32_t kernel
   void* y = out->data;
   const int ih = (int)IH, iw = (int)IW, oh = (int)eoh, ow = (int)eow;
   std::string name;
+  // Consecutive records of the same "same-size" pool, each pooling the
+  // previous output (the SPPF block of YOLO-style detectors), fold into the
+  // previous command: one pass computes the 2 or 3 outputs.  The outputs must
+  // not overlap the input or each other (the folded launch reads only x).
+  const bool same = KH == KW && (KH & 1) && sH == 1 && sW == 1 && pH == KH / 2 && pW == KW / 2 && dH == 1 &&
+                    dW == 1 && oh == ih && ow == iw && max_pool_chain_lds(ih, iw, KH / 2, 3) <= 64 * 1024;
+  const size_t bytes = (size_t)BC * ih * iw * elsize(dt);
+  auto disjoint = [](const void* a, const void* b, size_t n) {
+    const char *pa = static_cast<const char*>(a), *pb = static_cast<const char*>(b);
+    return pa + n <= pb || pb + n <= pa;
+  };
+  auto& pc = c->pool;
+  if (same && pc.cmd >= 0 && pc.cmd == (int)c->cmds.size() - 1 && pc.n < 3 && pc.y[pc.n - 1] == x &&
+      pc.dt == dt && pc.BC == BC && pc.H == ih && pc.W == iw && pc.P == KH / 2) {
+    bool ok = disjoint(y, pc.x, bytes);
+    for (int k = 0; k < pc.n; ++k) ok = ok && disjoint(y, pc.y[k], bytes);
+    if (ok) {
+      pc.y[pc.n++] = y;
+      const auto q = pc;
+      launch_max_pool_chain(dt, BC, ih, iw, q.P, q.n, q.x, q.y[0], q.y[1], q.y[2], c->dry(), &name);
+      Cmd& last = c->cmds.back();
+      last.fn = [q](hipStream_t s) {
+        return launch_max_pool_chain(q.dt, q.BC, q.H, q.W, q.P, q.n, q.x, q.y[0], q.y[1], q.y[2], s, nullptr);
+      };
+      last.name = name;
+      for (const auto& u : c->cur_uses) last.uses.push_back(u);
+      c->last_kernel = name;
+      c->invalidate();
+      return WGX_OK;
+    }
+  }
   launch_max_pool(dt, BC, ih, iw, oh, ow, KH, KW, sH, sW, pH, pW, dH, dW, x, y, c->dry(), &name);
-  return c->push([=](hipStream_t s) {
+  const int r2 = c->push([=](hipStream_t s) {
     return launch_max_pool(dt, BC, ih, iw, oh, ow, KH, KW, sH, sW, pH, pW, dH, dW, x, y, s, nullptr);
   }, name);
+  if (r2 == WGX_OK && same && disjoint(x, y, bytes)) {
+    pc.cmd = (int)c->cmds.size() - 1;
+    pc.dt = dt;
+    pc.BC = BC;
+    pc.H = ih;
+    pc.W = iw;
+    pc.P = KH / 2;
+    pc.n = 1;
+    pc.x = x;
+    pc.y[0] = y;
+    pc.y[1] = pc.y[2] = nullptr;
+    pc.bytes = bytes;
+  }
+  return r2;
 }
 
 // ------------------------------------------------------------------ execution
@@ -984,6 +1038,7 @@ int wgx_sync(wgx_ctx* c) {
 int wgx_reset(wgx_ctx* c) {
   CTX_GUARD(c);
   c->cmds.clear();
+  c->pool.cmd = -1;
   c->invalidate();
   return WGX_OK;
 }
