@@ -131,6 +131,8 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     # at most 32 output channels: 32 x 32 wave-split tiles however many there are
     assert conv([1, 16, 160, 160], [16, 16, 3, 3], [1, 16, 160, 160], pad=(1, 1)) == "gemm_mfma_f16_32x32w4_conv_ws"
     assert conv([1, 16, 320, 320], [32, 16, 3, 3], [1, 32, 160, 160], (2, 2), (1, 1)) == "gemm_mfma_f16_32x32w4_conv_ws"
+    assert conv([1, 8, 129, 131], [24, 8, 3, 3], [1, 24, 129, 131], pad=(1, 1)) == "gemm_mfma_f16_32x32w4_conv_ws"
+    assert conv([1, 16, 160, 160], [16, 16, 3, 3], [1, 16, 160, 160], pad=(1, 1), dtype="float32") == "gemm_mfma_f32_64x64w4_conv"
     # without it, 100 output tiles for 256 CUs split K = 1152 into ranges (suffix _k<ranges>)
     monkeypatch.setenv("WGX_WS", "off")
     assert "_conv_k" in conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1))

@@ -268,6 +268,8 @@ CONV_SWEEP = [
     ((1, 3, 40, 36), (48, 3, 3, 3), (1, 1), (1, 1), (1, 1), 1),      # small-tap kernel, 48 of 64 channels
     ((2, 1, 17, 19), (20, 1, 5, 5), (2, 1), (2, 1), (1, 1), 1),      # small-tap, 25 taps, batch 2, ragged
     ((1, 2, 15, 15), (5, 2, 3, 3), (1, 2), (2, 1), (2, 2), 1),       # small-tap, dilation 2
+    ((1, 16, 160, 160), (16, 16, 3, 3), (1, 1), (1, 1), (1, 1), 1),  # <= 32 channels, 400 tiles: 32x32 wave-split (fp16)
+    ((1, 8, 129, 131), (24, 8, 3, 3), (1, 1), (1, 1), (1, 1), 1),    # the same, ragged: 24 channels, 265 tiles
 ]
 
 
