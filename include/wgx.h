@@ -31,10 +31,10 @@
 extern "C" {
 #endif
 
-/* Maximum tensor rank.  Replaces MAX_NDIM, src/tensor.ts:57. */
+/* Maximum tensor rank.  Replaces MAX_NDIM, src/tensor.ts:23. */
 #define WGX_MAX_NDIM 8
 
-/* Element types.  Replaces DType / DTYPE_BYTESIZE, src/tensor.ts:38-64
+/* Element types.  Replaces DType / DTYPE_BYTESIZE, src/tensor.ts:4-30
  * (bfloat16 is an addition of this library). */
 typedef enum {
   WGX_FLOAT32 = 0,
@@ -58,13 +58,13 @@ typedef enum {
 } wgx_status;
 
 /* Buffer usage bits, the subset of GPUBufferUsage the reference checks
- * (src/context.ts:9-11, src/tensor.ts:102-104,152-154). */
+ * (src/context.ts:9-11, src/tensor.ts:68-70,118-120). */
 #define WGX_USAGE_COPY_SRC 0x4u
 #define WGX_USAGE_COPY_DST 0x8u
 #define WGX_USAGE_STORAGE 0x80u
 
 /* A non-owning tensor view: device pointer + dtype + row-major contiguous
- * shape.  Replaces Tensor's (dtype, shape, buffer) triple, src/tensor.ts:77-105. */
+ * shape.  Replaces Tensor's (dtype, shape, buffer) triple, src/tensor.ts:43-101. */
 typedef struct {
   void* data;
   int32_t dtype;
@@ -132,9 +132,9 @@ int wgx_free(wgx_ctx* ctx, void* ptr);
 /* Size and usage of the owned buffer that contains ptr (0 / error if none). */
 int wgx_buffer_info(const wgx_ctx* ctx, const void* ptr, uint64_t* base_offset,
                     uint64_t* size, uint32_t* usage);
-/* Tensor.setData (src/tensor.ts:149-169): stream-ordered host-to-device copy. */
+/* Tensor.setData (src/tensor.ts:115-135): stream-ordered host-to-device copy. */
 int wgx_write(wgx_ctx* ctx, void* dst, const void* src, uint64_t bytes);
-/* Tensor.getData (src/tensor.ts:176-192): waits for submitted work, then
+/* Tensor.getData (src/tensor.ts:142-158): waits for submitted work, then
  * copies device-to-host. */
 int wgx_read(wgx_ctx* ctx, const void* src, void* dst, uint64_t bytes);
 
@@ -204,10 +204,29 @@ int wgx_record_split(wgx_ctx* ctx, const wgx_tensor* in, int dim, const wgx_tens
                      int n_outputs);
 /* aten.upsample_nearest2d.vec, integer-or-fractional scale from the shapes. */
 int wgx_record_upsample_nearest2d(wgx_ctx* ctx, const wgx_tensor* in, const wgx_tensor* out);
-/* aten.max_pool2d_with_indices.default (values only). */
+/* aten.max_pool2d_with_indices.default [in, kernel_size, stride, padding,
+ * dilation, ceil_mode, [values, indices]] (src/shaders/max-pool-2d/
+ * index.ts:41-106): values[b,c,oh,ow] is the first strictly greatest element
+ * of the window in row-major order (cells outside the image are skipped;
+ * the initial value is -65504 for float16, -3.4e38 otherwise) and
+ * indices[b,c,oh,ow] its flat position ih * IW + iw in the plane (0 when no
+ * element beats the initial value).  indices is int32 of the values' shape,
+ * or NULL to skip it.  The output size is floor (ceil with ceil_mode) of
+ * (I + 2p - d(K-1) - 1) / s, plus 1, at least 0 (index.ts:75-78). */
 int wgx_record_max_pool2d(wgx_ctx* ctx, const wgx_tensor* in, const int32_t kernel[2],
                           const int32_t stride[2], const int32_t padding[2],
-                          const int32_t dilation[2], const wgx_tensor* out);
+                          const int32_t dilation[2], int ceil_mode, const wgx_tensor* out,
+                          const wgx_tensor* indices);
+/* aten.permute_copy.default [in, dims, out] (src/shaders/permute/
+ * index.ts:33-99): out dim k is input dim dims[k] (negative dims count from
+ * the end); any dtype, out of the permuted shape. */
+int wgx_record_permute(wgx_ctx* ctx, const wgx_tensor* in, const int32_t* dims, int n_dims,
+                       const wgx_tensor* out);
+/* aten._softmax.default [in, dim, half_to_float, out] (src/shaders/softmax/
+ * index.ts:62-125): out = exp(x - max) / sum(exp(x - max)) along dim
+ * (negative counts from the end), float32 arithmetic for every dtype;
+ * out has the input's dtype and element count. */
+int wgx_record_softmax(wgx_ctx* ctx, const wgx_tensor* in, int dim, const wgx_tensor* out);
 
 /* ---------------------------------------------------------------- execution */
 
@@ -216,6 +235,20 @@ int wgx_record_max_pool2d(wgx_ctx* ctx, const wgx_tensor* in, const int32_t kern
 int wgx_submit(wgx_ctx* ctx);
 /* sync() (src/context.ts:377-380): wait for all submitted work. */
 int wgx_sync(wgx_ctx* ctx);
+/* The pieces of an asynchronous sync() (src/context.ts:377-380: a Promise
+ * that settles when the work submitted so far is done), for hosts that wait
+ * off their main thread.  wgx_fence_record marks the queue's current end
+ * (call it from the thread that records and submits); wgx_fence_wait blocks
+ * until the queue has passed that mark and may run on any thread, also while
+ * the context records or after it was destroyed, because it touches only the
+ * fence; wgx_fence_error gives the reason of a failed wait; the owner frees
+ * the fence with wgx_fence_destroy.  A host-only context's fence is always
+ * passed. */
+typedef struct wgx_fence wgx_fence;
+int wgx_fence_record(wgx_ctx* ctx, wgx_fence** out);
+int wgx_fence_wait(wgx_fence* fence);
+const char* wgx_fence_error(const wgx_fence* fence);
+void wgx_fence_destroy(wgx_fence* fence);
 /* reset() (src/context.ts:386-389): drop recorded commands, keep buffers. */
 int wgx_reset(wgx_ctx* ctx);
 /* Number of recorded commands. */

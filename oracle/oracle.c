@@ -248,7 +248,7 @@ void orc_conv2d_f64(const int* p, const float* x, const float* w, const float* b
  * Transposed conv2d (PyTorch F.conv_transpose2d semantics), written in
  * SCATTER form: every input pixel adds x*w into the outputs it reaches.  The
  * reference kernel is the gather form (src/shaders/convolution/
- * conv-transpose2d.wgsl.ts:137-190); using the other form here means the two
+ * conv-transpose2d.wgsl.ts:48-99); using the other form here means the two
  * formulations check each other.  w [IC, OC/groups, KH, KW]; OH/OW from p[].
  */
 void orc_conv_transpose2d_f64(const int* p, const float* x, const float* w, const float* bias,
@@ -296,9 +296,9 @@ void orc_conv_transpose2d_f64(const int* p, const float* x, const float* w, cons
  * mm / bmm, every variant (tiled, vec4, 64x64; f32 and f16).
  * All variants accumulate each output sequentially in k from a zero
  * accumulator of the storage type, one product then one add per step:
- *   mm-64x64.wgsl.ts:88-91 and mm-64x64-f16.wgsl.ts:205-208
+ *   mm-64x64.wgsl.ts:88-91 and mm-64x64-f16.wgsl.ts:90-93
  *     acc = acc + b0*a.x + b1*a.y + b2*a.z + b3*a.w   (left to right)
- *   mm-vec4.wgsl.ts:162-170, mm-tiled.wgsl.ts:72-79 (acc + aval*b)
+ *   mm-vec4.wgsl.ts:76 (the same four-term form), mm-tiled.wgsl.ts:72-79 (acc + aval*b)
  *   bmm-64x64 / bmm-vec4 / bmm-tiled: the same bodies per batch.
  * Zero-padded tails add 0*0, which leaves the accumulator unchanged, so the
  * variant choice (mm/index.ts:65-78) does not change the result.

@@ -17,7 +17,9 @@ the ops the reference registers:
   aten.cat.default             concatenation        (src/shaders/cat)
   aten.split_with_sizes_copy   split along dim      (src/shaders/split-with-sizes)
   aten.upsample_nearest2d.vec  out[i] = in[floor(i * in / out)]  (src/shaders/upsample-nearest-2d)
-  aten.max_pool2d_with_indices values only, -inf padding  (src/shaders/max-pool-2d)
+  aten.max_pool2d_with_indices values and int32 indices (oracle/ops.py, src/shaders/max-pool-2d)
+  aten.permute_copy.default    transpose by dims   (oracle/ops.py, src/shaders/permute)
+  aten._softmax.default        exp(x-max)/sum      (oracle/ops.py, src/shaders/softmax)
   view / clone / squeeze / unsqueeze / prepack   byte copies
 
 Memory-plan pools are not modelled: values live in their own arrays, which is
@@ -29,7 +31,7 @@ from typing import Dict, List
 
 import numpy as np
 
-from . import conv2d_f64
+from . import conv2d_f64, ops
 
 _NP = {"float16": np.float16, "float32": np.float32, "int32": np.int32, "int64": np.int64}
 
@@ -106,19 +108,17 @@ def evaluate(program: dict, weights: bytes, inputs: List[np.ndarray]) -> List[np
             put(a[-1], x[:, :, ri][:, :, :, ci])
         elif name == "aten.max_pool2d_with_indices.default":
             x = arg(a[0])
-            k, s, p, d = arg(a[1]), arg(a[2]), arg(a[3]), arg(a[4])
-            s = s if s else k
+            hw = lambda v: (v[0], v[0]) if len(v) == 1 else tuple(v)
+            k, s, p, d = hw(arg(a[1])), hw(arg(a[2])), hw(arg(a[3])), hw(arg(a[4]))
             outs = vals[a[6]]["items"]
-            oshape = vals[outs[0]]["shape"]
-            xp = np.pad(x, ((0, 0), (0, 0), (p[0], p[0]), (p[1], p[1])), constant_values=-np.inf)
-            out = np.full(oshape, -np.inf)
-            oh, ow = oshape[2:]
-            for kh in range(k[0]):
-                for kw in range(k[1]):
-                    r0, c0 = kh * d[0], kw * d[1]
-                    win = xp[:, :, r0:r0 + s[0] * oh:s[0], c0:c0 + s[1] * ow:s[1]]
-                    out = np.maximum(out, win)
-            put(outs[0], out)
+            y, ix = ops.max_pool2d_with_indices(x, k, s, p, d, bool(arg(a[5])), vals[outs[0]]["dtype"])
+            put(outs[0], y)
+            if len(outs) > 1:
+                env[outs[1]] = ix.astype(np.float64)
+        elif name == "aten.permute_copy.default":
+            put(a[-1], ops.permute(arg(a[0]), arg(a[1])))
+        elif name == "aten._softmax.default":
+            put(a[-1], ops.softmax_f64(arg(a[0]), int(arg(a[1]))))
         elif name in ("aten.view_copy.default", "aten.clone.default", "aten.squeeze_copy.dims",
                       "aten.unsqueeze_copy.default", "et_vk.prepack.default"):
             put(a[-1], arg(a[0]).reshape(vals[a[-1]]["shape"]))

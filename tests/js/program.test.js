@@ -169,6 +169,47 @@ describe('recordProgram views', () => {
     deep.values[5] = S(-2);
     expect(elidedOf(deep)).toEqual([2]);
   });
+  // o1 = a + b, o2 = a * b, o3 = o1 + o2, all three program outputs
+  const threeOut = () => ({
+    version: '1',
+    chain: [
+      { name: 'aten.add.Tensor', args: [0, 1, 2, 3] },
+      { name: 'aten.mul.Tensor', args: [0, 1, 4] },
+      { name: 'aten.add.Tensor', args: [3, 4, 2, 5] },
+    ],
+    values: [
+      { type: 'tensor', shape: [4], dtype: 'float32', memObjId: 0 },
+      { type: 'tensor', shape: [4], dtype: 'float32', memObjId: 1 },
+      { type: 'scalar', value: 1 },
+      { type: 'tensor', shape: [4], dtype: 'float32', memObjId: 2 },
+      { type: 'tensor', shape: [4], dtype: 'float32', memObjId: 3 },
+      { type: 'tensor', shape: [4], dtype: 'float32', memObjId: 4 },
+    ],
+    inputIds: [0, 1],
+    outputIds: [3, 4, 5],
+    memoryPlan: { pools: [0, 1, 2, 3, 4].map((id) => ({ id, size: 16 })) },
+  });
+  it('binds no tensor when two program outputs share memory', async () => {
+    const ctx = new WgpuExecutionContext(await setupGPU());
+    const a = ctx.tensor('float32', [4]).setData(new Float32Array([1, 2, 3, 4]));
+    const b = ctx.tensor('float32', [4]).setData(new Float32Array([5, 6, 7, 8]));
+    const t = ctx.tensor('float32', [4]);
+    const u = ctx.tensor('float32', [4]);
+    ctx.recordProgram(threeOut(), weights, [a, b, t, t, u]);
+    // 3 ops, 2 input copies, 3 output copies: nothing is bound
+    expect(ctx.commandCount).toBe(8);
+    const ok = new WgpuExecutionContext(await setupGPU());
+    ok.recordProgram(threeOut(), weights, [a, b, ok.tensor('float32', [4]), ok.tensor('float32', [4]), ok.tensor('float32', [4])]);
+    expect(ok.commandCount).toBe(3);  // disjoint outputs: every input and output bound
+    ok.destroy();
+    if (ctx.device.index >= 0) {
+      ctx.submit();
+      await ctx.sync();
+      await expectTensorClose(W, t, [5, 12, 21, 32]);  // the later copy (o2) wins
+      await expectTensorClose(W, u, [11, 20, 31, 44]);
+    }
+    ctx.destroy();
+  });
   it('runs split/cat chains with and without views', async () => {
     const x = new Float32Array(16).map((_, i) => i - 5.5);
     const t = x.map((v) => 2 * v);

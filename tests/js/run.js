@@ -5,7 +5,7 @@ const path = require('path');
 const H = require('./harness');
 const gpu = process.argv.includes('--gpu');
 global.WGX_DEVICE_INDEX = gpu ? 0 : -1;
-for (const f of ['api.test.js', 'shaders.test.js', 'program.test.js']) require(path.join(__dirname, f));
+for (const f of ['api.test.js', 'shaders.test.js', 'ops.test.js', 'program.test.js']) require(path.join(__dirname, f));
 (async () => {
   let pass = 0; let fail = 0; let skip = 0;
   for (const t of H.tests) {

@@ -1,5 +1,5 @@
 """GPU tests of the execution model: submit/sync/reset semantics, copies,
-setData prefixes and graph replays (src/context.ts:172-389, src/tensor.ts:149-192).
+setData prefixes and graph replays (src/context.ts:172-389, src/tensor.ts:115-158).
 """
 import numpy as np
 import pytest

@@ -306,3 +306,64 @@ def test_emu_f32_gemm_within_fp64_bound(orc):
     C, Ca = orc.gemm_f64(A, B)
     E = orc.emu_gemm(0, A, B)
     assert np.all(np.abs(E - C) <= 512 * 2**-24 * Ca)
+
+
+# ------------------------------------------------------------ oracle/ops.py pins
+def test_max_pool_kats_and_torch(orc):
+    """max_pool2d_with_indices: the reference KATs (tests/shaders/max-pool-2d.test.ts:6-44),
+    torch's values and indices on tie-free inputs, and the first-of-equal rule
+    on a constant plane (closed form: the first in-image cell of each window)."""
+    from oracle import ops
+
+    x = np.arange(1, 17, dtype=np.float64).reshape(1, 1, 4, 4)
+    v, i = ops.max_pool2d_with_indices(x, (2, 2), (2, 2), (0, 0), (1, 1))
+    assert v.ravel().tolist() == [6, 8, 14, 16] and i.ravel().tolist() == [5, 7, 13, 15]
+    v, i = ops.max_pool2d_with_indices(np.array([1, 2, 3, 4.0]).reshape(1, 1, 2, 2), (3, 3), (1, 1), (1, 1), (1, 1))
+    assert v.ravel().tolist() == [4, 4, 4, 4] and i.ravel().tolist() == [3, 3, 3, 3]
+    rs = np.random.default_rng(5)
+    for shape, k, s, p, d in [((2, 3, 17, 23), (3, 3), (2, 2), (1, 1), (1, 1)),
+                              ((1, 4, 16, 15), (2, 3), (2, 1), (0, 1), (2, 1)),
+                              ((1, 128, 20, 20), (5, 5), (1, 1), (2, 2), (1, 1)),
+                              ((1, 2, 9, 9), (4, 4), (3, 3), (1, 2), (1, 1))]:
+        x = rs.permutation(int(np.prod(shape))).astype(np.float64).reshape(shape)  # distinct values
+        for ceil in (False, True):
+            v, i = ops.max_pool2d_with_indices(x, k, s, p, d, ceil)
+            tv, ti = F.max_pool2d(torch.from_numpy(x), k, s, p, d, ceil_mode=ceil, return_indices=True)
+            if tuple(tv.shape) != v.shape:  # torch drops a last window that starts in the padding
+                continue
+            assert np.array_equal(v, tv.numpy()) and np.array_equal(i, ti.numpy())
+    c = np.full((1, 1, 5, 7), 3.0)
+    v, i = ops.max_pool2d_with_indices(c, (3, 3), (2, 2), (1, 1), (1, 1))
+    for oh in range(v.shape[2]):
+        for ow in range(v.shape[3]):
+            assert i[0, 0, oh, ow] == max(0, oh * 2 - 1) * 7 + max(0, ow * 2 - 1)
+    # -inf and NaN never win; a window with nothing greater than the floor keeps it
+    y = np.array([[[[-np.inf, np.nan], [np.nan, -np.inf]]]])
+    v, i = ops.max_pool2d_with_indices(y, (2, 2), (1, 1), (0, 0), (1, 1), dtype="float16")
+    assert v.ravel().tolist() == [-65504.0] and i.ravel().tolist() == [0]
+    assert ops.pool_out_size(3, 2, 2, 0, 1, True) == 2 and ops.pool_out_size(3, 2, 2, 0, 1, False) == 1
+
+
+def test_softmax_and_permute_pins(orc):
+    """softmax_f64 against torch (float64) and the reference KATs
+    (tests/shaders/softmax.test.ts:6-80); permute against the reference KATs
+    (tests/shaders/permute.test.ts:6-69)."""
+    from oracle import ops
+
+    rs = np.random.default_rng(6)
+    for shape, dim in [((1, 2, 3), -1), ((2, 2), 0), ((3, 7, 5), 1), ((2, 400, 400), 2)]:
+        x = rs.standard_normal(shape) * 4
+        assert np.allclose(ops.softmax_f64(x, dim), torch.softmax(torch.from_numpy(x), dim).numpy(), rtol=1e-13, atol=0)
+        assert np.allclose(ops.softmax_f64(x, dim).sum(axis=dim), 1.0)
+    e = np.exp([1.0, 2, 3])
+    assert np.allclose(ops.softmax_f64(np.array([[1.0, 2, 3]]), -1), e / e.sum(), rtol=1e-15)
+    assert np.allclose(ops.softmax_f64(np.array([[1.0, 2], [3, 4]]), 0).ravel(),
+                       [np.exp(1) / (np.exp(1) + np.exp(3)), np.exp(2) / (np.exp(2) + np.exp(4)),
+                        np.exp(3) / (np.exp(1) + np.exp(3)), np.exp(4) / (np.exp(2) + np.exp(4))])
+    assert ops.permute(np.arange(1, 7).reshape(2, 3), [1, 0]).ravel().tolist() == [1, 4, 2, 5, 3, 6]
+    assert ops.permute(np.arange(1, 13).reshape(1, 2, 2, 3), [0, 1, 3, 2]).ravel().tolist() == \
+        [1, 4, 2, 5, 3, 6, 7, 10, 8, 11, 9, 12]
+    m = np.array([[r * 100 + c for c in range(48)] for r in range(64)])
+    assert np.array_equal(ops.permute(m, [1, 0]), m.T)
+    with pytest.raises(ValueError):
+        ops.permute(m, [0, 0])

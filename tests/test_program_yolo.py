@@ -155,6 +155,39 @@ def _expected_view_copies(prog):
     return n
 
 
+def _pool_chain_launches_saved(prog, views):
+    """Launches the runtime saves by folding the SPPF block's chained same-size
+    max-pools (pool k+1 reads pool k's values) into one: a pool joins only if
+    its values and indices outputs are disjoint from the chain's input and
+    from every earlier output (indices may repeat one region exactly).  Pool
+    tensors overlap when they share a memory-plan pool; with views, the
+    values of the block (pieces of the channel concatenation that follows)
+    live in the view slab, apart from every pool."""
+    vals, chain = prog["values"], prog["chain"]
+    ks = [k for k, op in enumerate(chain) if op["name"] == "aten.max_pool2d_with_indices.default"]
+    saved, k = 0, 0
+    while k < len(ks):
+        x = chain[ks[k]]["args"][0]
+        region = lambda t: ("view", t) if views and vals[t]["dtype"] != "int32" else ("pool", vals[t]["memObjId"])
+        ys, ids = [], []
+        j = k
+        while j < len(ks) and ks[j] == ks[k] + (j - k) and len(ys) < 3:
+            y, ix = vals[chain[ks[j]]["args"][-1]]["items"]
+            if ys and chain[ks[j]]["args"][0] != ys[-1]:
+                break
+            taken = {region(x)} | {region(t) for t in ys} | {region(t) for t in ids}
+            if ys and (region(y) in taken or (region(ix) in taken and region(ix) not in {region(t) for t in ids})):
+                break
+            if not ys and len({region(x), region(y), region(ix)}) < 3:
+                break
+            ys.append(y)
+            ids.append(ix)
+            j += 1
+        saved += max(0, len(ys) - 1)
+        k = max(j, k + 1)
+    return saved
+
+
 @needs_node
 def test_js_host_records_the_program(Y, tmp_path):
     Y.write(str(tmp_path), img=160)
@@ -173,9 +206,12 @@ def test_js_host_records_the_program(Y, tmp_path):
     n, adds = _expected_silu_fusions(prog)
     v = _expected_view_copies(prog)
     assert n > 0 and adds > 0 and v > 0
+    # the SPPF pools fold as far as their memory allows in each layout
+    pv, pn = _pool_chain_launches_saved(prog, True), _pool_chain_launches_saved(prog, False)
+    assert pv == 2
     assert base - res[("--no-views",)]["commands"] == 2 * n + adds
-    assert base - res[("--no-fuse",)]["commands"] == v
-    assert base - res[()]["commands"] == 2 * n + adds + v
+    assert base - res[("--no-fuse",)]["commands"] == v + pv - pn
+    assert base - res[()]["commands"] == 2 * n + adds + v + pv - pn
     # the caller's input and output tensors bound in place: two copies fewer
     cmd = [NODE, RUNNER, str(tmp_path), "--device", "-1", "--record-only", "--no-bind-io"]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)

@@ -2,7 +2,7 @@
 // convolution with 1 < groups (not depthwise) and transposed convolution.
 //
 // Reference: conv2d.wgsl.ts:44-89 (direct, one thread per output, general
-// groups) and conv-transpose2d.wgsl.ts:137-190 (gather form), selected by
+// groups) and conv-transpose2d.wgsl.ts:48-99 (gather form), selected by
 // src/shaders/convolution/index.ts:213-222.  Neither is on a benchmarked
 // configuration; these kernels exist so the convolution entry point accepts
 // everything the reference accepts.  One lane per output element, float32

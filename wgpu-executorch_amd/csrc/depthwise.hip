@@ -30,7 +30,7 @@
 //    (element-wise staging through LDS).  Correct for every shape the
 //    convolution driver accepts; used where the two above do not apply.
 // All three accumulate in fp32 in the reference's order: bias, then taps
-// kh-outer / kw-inner (conv2d-depthwise.wgsl.ts:228-268), rounded once.
+// kh-outer / kw-inner (conv2d-depthwise.wgsl.ts:56-128), rounded once.
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>

@@ -145,14 +145,35 @@ hipError_t launch_slab_copy(int elsize, long long outer, long long inner_src,
                             std::string* name);
 hipError_t launch_upsample_nearest(int dtype, int BC, int IH, int IW, int OH, int OW,
                                    const void* x, void* y, hipStream_t s, std::string* name);
-// n = 2 or 3 chained K x K max-pools (stride 1, padding P = K/2, dilation 1)
-// of one [BC, H, W] map in one pass: y1 = pool(x), y2 = pool(y1), y3 = pool(y2).
-// One block per plane, max_pool_chain_lds bytes of LDS (at most 64 KB).
-size_t max_pool_chain_lds(int H, int W, int P, int n);
-hipError_t launch_max_pool_chain(int dtype, int BC, int H, int W, int P, int n, const void* x, void* y1, void* y2,
-                                 void* y3, hipStream_t s, std::string* name);
+// n = 2 or 3 chained K x K max-pools (K = 2P + 1, stride 1, padding P,
+// dilation 1) of one [BC, H, W] map in one pass: y1 = pool(x), y2 =
+// pool(y1), y3 = pool(y2), each with its int32 indices into the plane it
+// pooled (idx[k] may be null).  One block per plane, max_pool_chain_lds
+// bytes of LDS (at most 64 KB).
+size_t max_pool_chain_lds(int H, int W, int P);
+hipError_t launch_max_pool_chain(int dtype, int BC, int H, int W, int P, int n, const void* x, void* const y[3],
+                                 int32_t* const idx[3], hipStream_t s, std::string* name);
+// max_pool2d_with_indices: values y and, when idx is not null, the int32
+// flat index ih * IW + iw of each window's first strictly greatest element.
 hipError_t launch_max_pool(int dtype, int BC, int IH, int IW, int OH, int OW, int KH, int KW,
                            int sH, int sW, int pH, int pW, int dH, int dW, const void* x,
-                           void* y, hipStream_t s, std::string* name);
+                           void* y, int32_t* idx, hipStream_t s, std::string* name);
+
+// permute_copy of a contiguous tensor: out dim k is input dim perm[k].
+// out_shape / src_stride are filled by launch_permute.
+struct PermuteDesc {
+  int elsize;
+  int ndim;
+  int perm[WGX_MAX_NDIM];
+  long long in_shape[WGX_MAX_NDIM];
+  long long out_shape[WGX_MAX_NDIM];
+  long long src_stride[WGX_MAX_NDIM];
+  const void* x;
+  void* y;
+};
+hipError_t launch_permute(const PermuteDesc& d, hipStream_t s, std::string* name);
+// softmax of a contiguous [outer, r, inner] view along r.
+hipError_t launch_softmax(int dtype, long long outer, long long r, long long inner, const void* x, void* y,
+                          hipStream_t s, std::string* name);
 
 }  // namespace wgx

@@ -126,7 +126,8 @@ struct wgx_ctx {
     int dt, BC, H, W, P, n;
     const void* x;
     void* y[3];
-    size_t bytes;  // of x and of every output
+    int32_t* idx[3];  // indices outputs (null: none)
+    size_t bytes;     // of x and of every values output
   } pool;
 
   int fail(int code, const char* fmt, ...) {
@@ -910,50 +911,77 @@ int wgx_record_upsample_nearest2d(wgx_ctx* c, const wgx_tensor* in, const wgx_te
 }
 
 int wgx_record_max_pool2d(wgx_ctx* c, const wgx_tensor* in, const int32_t kernel[2], const int32_t stride[2],
-                          const int32_t padding[2], const int32_t dilation[2], const wgx_tensor* out) {
+                          const int32_t padding[2], const int32_t dilation[2], int ceil_mode, const wgx_tensor* out,
+                          const wgx_tensor* indices) {
   CTX_GUARD(c);
   int r;
   if ((r = c->check(in, "max_pool2d: in")) || (r = c->check(out, "max_pool2d: out"))) return r;
+  if (indices && (r = c->check(indices, "max_pool2d: indices"))) return r;
   if (!float_dt(in->dtype) || out->dtype != in->dtype || in->ndim != 4 || out->ndim != 4)
     return c->fail(WGX_ERR_INVALID, "max_pool2d: expected 4D float tensors");
+  if (!kernel || !stride || !padding || !dilation)
+    return c->fail(WGX_ERR_INVALID, "max_pool2d: kernel, stride, padding and dilation are required");
   const int KH = kernel[0], KW = kernel[1], sH = stride[0], sW = stride[1], pH = padding[0], pW = padding[1];
   const int dH = dilation[0], dW = dilation[1];
   if (KH <= 0 || KW <= 0 || sH <= 0 || sW <= 0 || dH <= 0 || dW <= 0 || pH < 0 || pW < 0)
     return c->fail(WGX_ERR_INVALID, "max_pool2d: invalid kernel/stride/padding/dilation");
   const long long IH = in->shape[2], IW = in->shape[3];
-  const long long eoh = (IH + 2LL * pH - (long long)dH * (KH - 1) - 1) / sH + 1;
-  const long long eow = (IW + 2LL * pW - (long long)dW * (KW - 1) - 1) / sW + 1;
+  // floor or ceil of the window count, at least 0 (max-pool-2d/index.ts:73-78)
+  auto count = [&](long long num, int s) {
+    const long long q = ceil_mode ? (num >= 0 ? (num + s - 1) / s : -((-num) / s)) : (num >= 0 ? num / s : -((-num + s - 1) / s));
+    return q + 1 < 0 ? 0LL : q + 1;
+  };
+  const long long eoh = count(IH + 2LL * pH - ((long long)dH * (KH - 1) + 1), sH);
+  const long long eow = count(IW + 2LL * pW - ((long long)dW * (KW - 1) + 1), sW);
   if (out->shape[0] != in->shape[0] || out->shape[1] != in->shape[1] || out->shape[2] != eoh || out->shape[3] != eow)
     return c->fail(WGX_ERR_INVALID, "max_pool2d: expected output spatial [%lld, %lld]", eoh, eow);
+  if (indices) {
+    if (indices->dtype != WGX_INT32) return c->fail(WGX_ERR_INVALID, "max_pool2d: indices output must be int32");
+    if (indices->ndim != 4)
+      return c->fail(WGX_ERR_INVALID, "max_pool2d: indices output must have the values' shape");
+    for (int k = 0; k < 4; ++k)
+      if (indices->shape[k] != out->shape[k])
+        return c->fail(WGX_ERR_INVALID, "max_pool2d: indices output must have the values' shape");
+  }
   const int dt = in->dtype;
   const int BC = (int)(in->shape[0] * in->shape[1]);
   const void* x = in->data;
   void* y = out->data;
+  int32_t* ix = indices ? static_cast<int32_t*>(indices->data) : nullptr;
   const int ih = (int)IH, iw = (int)IW, oh = (int)eoh, ow = (int)eow;
   std::string name;
   // Consecutive records of the same "same-size" pool, each pooling the
   // previous output (the SPPF block of YOLO-style detectors), fold into the
-  // previous command: one pass computes the 2 or 3 outputs.  The outputs must
-  // not overlap the input or each other (the folded launch reads only x).
+  // previous command: one launch writes the 2 or 3 levels.  The folded
+  // launch reads x once, up front, per plane, and then writes every level,
+  // so each output must be disjoint from x and from every other output
+  // (index outputs may also be the very same memory: a lane writes the
+  // levels of a pixel in order, so the last level's index stays, as after
+  // separate launches).
   const bool same = KH == KW && (KH & 1) && sH == 1 && sW == 1 && pH == KH / 2 && pW == KW / 2 && dH == 1 &&
-                    dW == 1 && oh == ih && ow == iw && max_pool_chain_lds(ih, iw, KH / 2, 3) <= 64 * 1024;
-  const size_t bytes = (size_t)BC * ih * iw * elsize(dt);
-  auto disjoint = [](const void* a, const void* b, size_t n) {
+                    dW == 1 && oh == ih && ow == iw && max_pool_chain_lds(ih, iw, KH / 2) <= 64 * 1024;
+  const size_t bytes = (size_t)BC * ih * iw * elsize(dt), ibytes = (size_t)BC * ih * iw * 4;
+  auto disjoint = [](const void* a, size_t na, const void* b, size_t nb) {
     const char *pa = static_cast<const char*>(a), *pb = static_cast<const char*>(b);
-    return pa + n <= pb || pb + n <= pa;
+    return !a || !b || pa + na <= pb || pb + nb <= pa;
   };
   auto& pc = c->pool;
   if (same && pc.cmd >= 0 && pc.cmd == (int)c->cmds.size() - 1 && pc.n < 3 && pc.y[pc.n - 1] == x &&
       pc.dt == dt && pc.BC == BC && pc.H == ih && pc.W == iw && pc.P == KH / 2) {
-    bool ok = disjoint(y, pc.x, bytes);
-    for (int k = 0; k < pc.n; ++k) ok = ok && disjoint(y, pc.y[k], bytes);
+    bool ok = disjoint(y, bytes, pc.x, bytes) && disjoint(ix, ibytes, pc.x, bytes) && disjoint(ix, ibytes, y, bytes);
+    for (int k = 0; k < pc.n; ++k) {
+      ok = ok && disjoint(y, bytes, pc.y[k], bytes) && disjoint(y, bytes, pc.idx[k], ibytes) &&
+           disjoint(ix, ibytes, pc.y[k], bytes) && (ix == pc.idx[k] || disjoint(ix, ibytes, pc.idx[k], ibytes));
+    }
     if (ok) {
-      pc.y[pc.n++] = y;
+      pc.y[pc.n] = y;
+      pc.idx[pc.n] = ix;
+      pc.n++;
       const auto q = pc;
-      launch_max_pool_chain(dt, BC, ih, iw, q.P, q.n, q.x, q.y[0], q.y[1], q.y[2], c->dry(), &name);
+      launch_max_pool_chain(dt, BC, ih, iw, q.P, q.n, q.x, q.y, q.idx, c->dry(), &name);
       Cmd& last = c->cmds.back();
       last.fn = [q](hipStream_t s) {
-        return launch_max_pool_chain(q.dt, q.BC, q.H, q.W, q.P, q.n, q.x, q.y[0], q.y[1], q.y[2], s, nullptr);
+        return launch_max_pool_chain(q.dt, q.BC, q.H, q.W, q.P, q.n, q.x, q.y, q.idx, s, nullptr);
       };
       last.name = name;
       for (const auto& u : c->cur_uses) last.uses.push_back(u);
@@ -962,11 +990,12 @@ int wgx_record_max_pool2d(wgx_ctx* c, const wgx_tensor* in, const int32_t kernel
       return WGX_OK;
     }
   }
-  launch_max_pool(dt, BC, ih, iw, oh, ow, KH, KW, sH, sW, pH, pW, dH, dW, x, y, c->dry(), &name);
+  launch_max_pool(dt, BC, ih, iw, oh, ow, KH, KW, sH, sW, pH, pW, dH, dW, x, y, ix, c->dry(), &name);
   const int r2 = c->push([=](hipStream_t s) {
-    return launch_max_pool(dt, BC, ih, iw, oh, ow, KH, KW, sH, sW, pH, pW, dH, dW, x, y, s, nullptr);
+    return launch_max_pool(dt, BC, ih, iw, oh, ow, KH, KW, sH, sW, pH, pW, dH, dW, x, y, ix, s, nullptr);
   }, name);
-  if (r2 == WGX_OK && same && disjoint(x, y, bytes)) {
+  if (r2 == WGX_OK && same && disjoint(x, bytes, y, bytes) && disjoint(x, bytes, ix, ibytes) &&
+      disjoint(y, bytes, ix, ibytes)) {
     pc.cmd = (int)c->cmds.size() - 1;
     pc.dt = dt;
     pc.BC = BC;
@@ -977,9 +1006,72 @@ int wgx_record_max_pool2d(wgx_ctx* c, const wgx_tensor* in, const int32_t kernel
     pc.x = x;
     pc.y[0] = y;
     pc.y[1] = pc.y[2] = nullptr;
+    pc.idx[0] = ix;
+    pc.idx[1] = pc.idx[2] = nullptr;
     pc.bytes = bytes;
   }
   return r2;
+}
+
+int wgx_record_permute(wgx_ctx* c, const wgx_tensor* in, const int32_t* dims, int n_dims, const wgx_tensor* out) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(in, "permute: in")) || (r = c->check(out, "permute: out"))) return r;
+  if (out->dtype != in->dtype) return c->fail(WGX_ERR_INVALID, "permute: input and output dtypes differ");
+  const int rank = in->ndim;
+  if (out->ndim != rank) return c->fail(WGX_ERR_INVALID, "permute: output rank != input rank");
+  if (n_dims != rank || (rank > 0 && !dims))
+    return c->fail(WGX_ERR_INVALID, "permute: dims count (%d) != input rank (%d)", n_dims, rank);
+  PermuteDesc d{};
+  d.elsize = elsize(in->dtype);
+  d.ndim = rank;
+  unsigned seen = 0;
+  for (int k = 0; k < rank; ++k) {
+    int p = dims[k] < 0 ? dims[k] + rank : dims[k];
+    if (p < 0 || p >= rank || (seen >> p & 1u)) return c->fail(WGX_ERR_INVALID, "permute: invalid permute dims");
+    seen |= 1u << p;
+    d.perm[k] = p;
+    d.in_shape[k] = in->shape[k];
+  }
+  for (int k = 0; k < rank; ++k)
+    if (out->shape[k] != in->shape[d.perm[k]])
+      return c->fail(WGX_ERR_INVALID, "permute: output shape does not match permuted input shape");
+  d.x = in->data;
+  d.y = out->data;
+  const uintptr_t xb = reinterpret_cast<uintptr_t>(in->data), yb = reinterpret_cast<uintptr_t>(out->data);
+  const uintptr_t nb = (uintptr_t)numel(in) * d.elsize;
+  if (xb < yb + nb && yb < xb + nb) return c->fail(WGX_ERR_INVALID, "permute: output overlaps the input");
+  std::string name;
+  launch_permute(d, c->dry(), &name);
+  return c->push([d](hipStream_t s) { return launch_permute(d, s, nullptr); }, name);
+}
+
+int wgx_record_softmax(wgx_ctx* c, const wgx_tensor* in, int dim, const wgx_tensor* out) {
+  CTX_GUARD(c);
+  int r;
+  if ((r = c->check(in, "softmax: in")) || (r = c->check(out, "softmax: out"))) return r;
+  if (!float_dt(in->dtype) || out->dtype != in->dtype)
+    return c->fail(WGX_ERR_INVALID, "softmax: Tensors must have matching float dtype");
+  if (in->ndim == 0) return c->fail(WGX_ERR_INVALID, "softmax: scalar input unsupported");
+  if (numel(in) != numel(out)) return c->fail(WGX_ERR_INVALID, "softmax: input/output numel mismatch");
+  const int d = norm_dim(dim, in->ndim);
+  if (d < 0 || d >= in->ndim) return c->fail(WGX_ERR_INVALID, "softmax: dim out of range");
+  long long outer = 1, inner = 1;
+  for (int k = 0; k < d; ++k) outer *= in->shape[k];
+  for (int k = d + 1; k < in->ndim; ++k) inner *= in->shape[k];
+  const long long rr = in->shape[d];
+  const int dt = in->dtype;
+  const void* x = in->data;
+  void* y = out->data;
+  // a line is read twice (max/sum, then the outputs): the output may be the
+  // input itself, but must not overlap it otherwise
+  const uintptr_t xb = reinterpret_cast<uintptr_t>(x), yb = reinterpret_cast<uintptr_t>(y);
+  const uintptr_t nb = (uintptr_t)numel(in) * elsize(dt);
+  if (xb != yb && xb < yb + nb && yb < xb + nb)
+    return c->fail(WGX_ERR_INVALID, "softmax: output partly overlaps the input");
+  std::string name;
+  launch_softmax(dt, outer, rr, inner, x, y, c->dry(), &name);
+  return c->push([=](hipStream_t s) { return launch_softmax(dt, outer, rr, inner, x, y, s, nullptr); }, name);
 }
 
 // ------------------------------------------------------------------ execution
@@ -1033,6 +1125,56 @@ int wgx_sync(wgx_ctx* c) {
   if (!c->d->has_dev) return WGX_OK;
   hipError_t e = hipStreamSynchronize(c->d->stream);
   return e == hipSuccess ? WGX_OK : c->hip_fail(e, "sync");
+}
+
+}  // extern "C"
+
+struct wgx_fence {
+  int device = -1;
+  hipEvent_t ev = nullptr;  // null: nothing to wait for (host-only context)
+  std::string err;
+};
+
+extern "C" {
+
+int wgx_fence_record(wgx_ctx* c, wgx_fence** out) {
+  CTX_GUARD(c);
+  if (!out) return c->fail(WGX_ERR_INVALID, "sync: out is NULL");
+  *out = nullptr;
+  wgx_fence* f = new wgx_fence();
+  if (c->d->has_dev) {
+    f->device = c->d->device;
+    hipError_t e = hipEventCreateWithFlags(&f->ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(f->ev, c->d->stream);
+    if (e != hipSuccess) {
+      if (f->ev) hipEventDestroy(f->ev);
+      delete f;
+      return c->hip_fail(e, "sync");
+    }
+  }
+  *out = f;
+  return WGX_OK;
+}
+
+int wgx_fence_wait(wgx_fence* f) {
+  if (!f) return WGX_ERR_INVALID;
+  if (!f->ev) return WGX_OK;
+  hipSetDevice(f->device);
+  const hipError_t e = hipEventSynchronize(f->ev);
+  if (e == hipSuccess) return WGX_OK;
+  f->err = std::string("sync: ") + hipGetErrorString(e);
+  return WGX_ERR_HIP;
+}
+
+const char* wgx_fence_error(const wgx_fence* f) { return f ? f->err.c_str() : "null fence"; }
+
+void wgx_fence_destroy(wgx_fence* f) {
+  if (!f) return;
+  if (f->ev) {
+    hipSetDevice(f->device);
+    hipEventDestroy(f->ev);
+  }
+  delete f;
 }
 
 int wgx_reset(wgx_ctx* c) {

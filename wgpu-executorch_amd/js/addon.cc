@@ -403,20 +403,59 @@ napi_value record_upsample(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
-// recordMaxPool2d(h, in, kernel, stride, padding, dilation, out)
+// recordMaxPool2d(h, in, kernel, stride, padding, dilation, ceilMode, values, indices|null)
 napi_value record_max_pool(napi_env env, napi_callback_info info) {
   Args a;
-  if (!get_args(env, info, a, 7)) return nullptr;
+  if (!get_args(env, info, a, 9)) return nullptr;
   wgx_ctx* c = handle(env, a.argv[0]);
   if (!c) return nullptr;
-  wgx_tensor x, o;
-  if (!to_tensor(env, a.argv[1], x) || !to_tensor(env, a.argv[6], o)) return nullptr;
+  wgx_tensor x, o, ix;
+  if (!to_tensor(env, a.argv[1], x) || !to_tensor(env, a.argv[7], o)) return nullptr;
+  const bool has_idx = !is_nullish(env, a.argv[8]);
+  if (has_idx && !to_tensor(env, a.argv[8], ix)) return nullptr;
   int32_t k[2], s[2], p[2], d[2];
   pair2(env, a.argv[2], k);
   pair2(env, a.argv[3], s);
   pair2(env, a.argv[4], p);
   pair2(env, a.argv[5], d);
-  if (!ok(env, c, wgx_record_max_pool2d(c, &x, k, s, p, d, &o))) return nullptr;
+  if (!ok(env, c, wgx_record_max_pool2d(c, &x, k, s, p, d, i32(env, a.argv[6]), &o, has_idx ? &ix : nullptr)))
+    return nullptr;
+  return undefined(env);
+}
+
+// recordPermute(h, in, dims, out)
+napi_value record_permute(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 4)) return nullptr;
+  wgx_ctx* c = handle(env, a.argv[0]);
+  if (!c) return nullptr;
+  wgx_tensor x, o;
+  if (!to_tensor(env, a.argv[1], x) || !to_tensor(env, a.argv[3], o)) return nullptr;
+  uint32_t n = 0;
+  napi_get_array_length(env, a.argv[2], &n);
+  if (n > WGX_MAX_NDIM) {
+    napi_throw_range_error(env, nullptr, "wgx: permute dims exceed rank 8");
+    return nullptr;
+  }
+  int32_t dims[WGX_MAX_NDIM] = {0};
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    napi_get_element(env, a.argv[2], i, &e);
+    dims[i] = i32(env, e);
+  }
+  if (!ok(env, c, wgx_record_permute(c, &x, dims, (int)n, &o))) return nullptr;
+  return undefined(env);
+}
+
+// recordSoftmax(h, in, dim, out)
+napi_value record_softmax(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 4)) return nullptr;
+  wgx_ctx* c = handle(env, a.argv[0]);
+  if (!c) return nullptr;
+  wgx_tensor x, o;
+  if (!to_tensor(env, a.argv[1], x) || !to_tensor(env, a.argv[3], o)) return nullptr;
+  if (!ok(env, c, wgx_record_softmax(c, &x, i32(env, a.argv[2]), &o))) return nullptr;
   return undefined(env);
 }
 
@@ -436,6 +475,61 @@ napi_value sync(napi_env env, napi_callback_info info) {
   wgx_ctx* c = handle(env, a.argv[0]);
   if (!c || !ok(env, c, wgx_sync(c))) return nullptr;
   return undefined(env);
+}
+
+// syncAsync(h) -> Promise: sync() / queue.onSubmittedWorkDone()
+// (src/context.ts:377-380).  A fence is recorded on the queue here, on the
+// JS thread; a libuv worker waits for it (the wait touches only the fence,
+// never the context, so recording may go on meanwhile) and the promise
+// settles back on the JS thread.
+struct SyncWork {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  wgx_fence* fence = nullptr;
+  int status = 0;
+};
+
+void sync_execute(napi_env, void* data) {
+  SyncWork* w = static_cast<SyncWork*>(data);
+  w->status = wgx_fence_wait(w->fence);
+}
+
+void sync_complete(napi_env env, napi_status st, void* data) {
+  SyncWork* w = static_cast<SyncWork*>(data);
+  if (st == napi_ok && w->status == 0) {
+    napi_resolve_deferred(env, w->deferred, undefined(env));
+  } else {
+    std::string msg = st == napi_ok ? wgx_fence_error(w->fence) : "sync: cancelled";
+    napi_value m, err;
+    napi_create_string_utf8(env, msg.c_str(), NAPI_AUTO_LENGTH, &m);
+    napi_create_error(env, nullptr, m, &err);
+    napi_reject_deferred(env, w->deferred, err);
+  }
+  wgx_fence_destroy(w->fence);
+  napi_delete_async_work(env, w->work);
+  delete w;
+}
+
+napi_value sync_async(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  wgx_ctx* c = handle(env, a.argv[0]);
+  if (!c) return nullptr;
+  wgx_fence* f = nullptr;
+  if (!ok(env, c, wgx_fence_record(c, &f))) return nullptr;
+  SyncWork* w = new SyncWork();
+  w->fence = f;
+  napi_value promise, name;
+  if (napi_create_promise(env, &w->deferred, &promise) != napi_ok ||
+      napi_create_string_utf8(env, "wgx_sync", NAPI_AUTO_LENGTH, &name) != napi_ok ||
+      napi_create_async_work(env, nullptr, name, sync_execute, sync_complete, w, &w->work) != napi_ok ||
+      napi_queue_async_work(env, w->work) != napi_ok) {
+    wgx_fence_destroy(f);
+    delete w;
+    napi_throw_error(env, nullptr, "wgx: could not queue the sync");
+    return nullptr;
+  }
+  return promise;
 }
 
 napi_value reset(napi_env env, napi_callback_info info) {
@@ -476,8 +570,10 @@ napi_value init(napi_env env, napi_value exports) {
              {"recordAdd", record_add},       {"recordMul", record_mul},
              {"recordUnary", record_unary},   {"recordCat", record_cat},
              {"recordSplit", record_split},   {"recordUpsampleNearest2d", record_upsample},
-             {"recordMaxPool2d", record_max_pool}, {"submit", submit},
-             {"sync", sync},                  {"reset", reset},
+             {"recordMaxPool2d", record_max_pool}, {"recordPermute", record_permute},
+             {"recordSoftmax", record_softmax}, {"submit", submit},
+             {"sync", sync},                  {"syncAsync", sync_async},
+             {"reset", reset},
              {"setGraphMode", set_graph_mode}, {"timeSubmits", time_submits}};
   for (const Fn& f : fns) {
     napi_value v;

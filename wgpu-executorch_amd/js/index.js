@@ -22,10 +22,10 @@ const GPUBufferUsage = Object.freeze({
   UNIFORM: 0x40, STORAGE: 0x80, INDIRECT: 0x100, QUERY_RESOLVE: 0x200,
 });
 
-/** src/tensor.ts:57 */
+/** src/tensor.ts:23 */
 const MAX_NDIM = 8;
 
-/** src/tensor.ts:60-64, plus bfloat16. */
+/** src/tensor.ts:26-30, plus bfloat16. */
 const DTYPE_BYTESIZE = Object.freeze({
   float32: 4, float16: 2, float64: 8, int32: 4, int64: 8, int8: 1, uint8: 1, bool: 1, bfloat16: 2,
 });
@@ -82,9 +82,9 @@ class WgxDevice {
         native.write(self._h, buffer.ptr + (offset || 0), ab, base + (dataOffset || 0),
           size === undefined ? ab.byteLength - base - (dataOffset || 0) : size);
       },
+      /** Settles when the work submitted so far is done (waited off the JS thread). */
       onSubmittedWorkDone() {
-        native.sync(self._h);
-        return Promise.resolve();
+        return native.syncAsync(self._h);
       },
     };
   }
@@ -111,7 +111,7 @@ function createDevice(index) {
   return new WgxDevice(index === undefined ? 0 : index);
 }
 
-/** A non-owning tensor view (src/tensor.ts:77-193). */
+/** A non-owning tensor view (src/tensor.ts:43-159). */
 class Tensor {
   constructor(dtype, shape, device, buffer) {
     if (shape.length > MAX_NDIM) {
@@ -146,7 +146,7 @@ class Tensor {
     return { ptr: this._buffer.ptr, dtype: DTYPE_CODE[this._dtype], shape: this._shape };
   }
 
-  /** src/tensor.ts:149-169: prefix write, padded to 4 bytes. */
+  /** src/tensor.ts:115-135: prefix write, padded to 4 bytes. */
   setData(src) {
     const byteLength = this.byteLength;
     if ((this._buffer.usage & GPUBufferUsage.COPY_DST) === 0) {
@@ -164,7 +164,7 @@ class Tensor {
     return this;
   }
 
-  /** src/tensor.ts:176-192: waits for submitted work, resolves the bytes. */
+  /** src/tensor.ts:142-158: waits for submitted work, resolves the bytes. */
   async getData() {
     return native.read(this._device._h, this._buffer.ptr, this.byteLength);
   }
@@ -235,7 +235,12 @@ class WgpuExecutionContext {
     if (dst.byteLength < src.byteLength) {
       throw new Error(`copy: destination (${dst.byteLength}B) < source (${src.byteLength}B)`);
     }
-    native.recordCopy(this._h, dst.buffer.ptr, src.buffer.ptr, src.byteLength);
+    // src/context.ts:182-189: the copy is padded to whole 4-byte words.  A
+    // buffer this backend carves out of a larger allocation (a view) may end
+    // at the tensor's last byte, and the bytes after it then belong to
+    // another tensor: the padding stops at the end of either buffer.
+    const padded = Math.ceil(src.byteLength / 4) * 4;
+    native.recordCopy(this._h, dst.buffer.ptr, src.buffer.ptr, Math.min(padded, src.buffer.size, dst.buffer.size));
     return this;
   }
 
@@ -324,14 +329,15 @@ class WgpuExecutionContext {
     if (!(options && options.bindIO === false)) {
       const writers = new Map();
       for (const op of program.chain) {
-        const outs = opOutputs(op, program.values);
-        if (op.name === 'aten.max_pool2d_with_indices.default' && op.args.length >= 2) {
-          outs.push(op.args[op.args.length - 2]);  // values and indices are both written
-        }
-        for (const id of outs) writers.set(id, (writers.get(id) || 0) + 1);
+        for (const id of opOutputs(op, program.values)) writers.set(id, (writers.get(id) || 0) + 1);
       }
       const ins = args.slice(0, numInputs), outs = args.slice(numInputs);
-      const ioClash = ins.some((a) => a instanceof Tensor && outs.some((o) => o instanceof Tensor && overlaps(a, o)));
+      // bound tensors must not share memory across the input / output
+      // boundary, and two outputs must not share memory either (the
+      // producer of one would overwrite the other while later ops still
+      // read it)
+      const ioClash = ins.some((a) => a instanceof Tensor && outs.some((o) => o instanceof Tensor && overlaps(a, o))) ||
+        outs.some((o, i) => o instanceof Tensor && outs.some((p, j) => j !== i && p instanceof Tensor && overlaps(o, p)));
       const fits = (t, id) => t instanceof Tensor && t.dtype === program.values[id].dtype &&
         t.byteLength === valueBytes(program.values[id]);
       const once = (ids) => (id) => ids.filter((x) => x === id).length === 1;
@@ -448,9 +454,14 @@ class WgpuExecutionContext {
     native.submit(this._h);
   }
 
+  /**
+   * src/context.ts:377-380: a Promise that settles when the work submitted
+   * so far is done.  The wait runs on a libuv worker, so the JS thread keeps
+   * running (and may record the next frame) meanwhile.
+   */
   async sync() {
     this._assertNotDestroyed();
-    native.sync(this._h);
+    await native.syncAsync(this._h);
   }
 
   reset() {
@@ -500,6 +511,54 @@ function resolveArgs(op, values, tensors) {
         return undefined;
       default:
         return undefined;
+    }
+  });
+}
+
+/**
+ * The converter's consistency rules for a program and its weights
+ * (utils/pte_to_program.py:421-475, same messages), for hosts that load
+ * converted files.  One relaxation: the weights may be longer than the sum
+ * of the declared constant lengths, since the float16 converter pads each
+ * constant to a 4-byte offset (utils/convert_model_to_fp16.mjs:61-66) and
+ * does not re-validate.  recordProgram itself keeps the reference's own
+ * checks and messages (src/context.ts:219-317).
+ */
+function validateProgram(program, weightsByteLength) {
+  const { values, chain } = program;
+  let declared = 0;
+  for (const v of values) if (v.type === 'tensor' && v.weightsLength !== undefined) declared += v.weightsLength;
+  if (declared > weightsByteLength) {
+    throw new Error(`Weights size mismatch: declared ${declared} bytes, actual ${weightsByteLength} bytes`);
+  }
+  chain.forEach((op, ci) => {
+    for (const arg of op.args) {
+      if (Number.isInteger(arg) && (arg < 0 || arg >= values.length)) {
+        throw new Error(`chain[${ci}] '${op.name}' references values[${arg}] but only ${values.length} values exist`);
+      }
+    }
+  });
+  for (const [label, ids] of [['inputIds', program.inputIds], ['outputIds', program.outputIds]]) {
+    for (const idx of ids) {
+      if (idx < 0 || idx >= values.length) throw new Error(`${label} references values[${idx}] out of range`);
+      if (values[idx].type !== 'tensor') {
+        throw new Error(`${label} references values[${idx}] of type '${values[idx].type}', expected 'tensor'`);
+      }
+    }
+  }
+  const poolIds = new Set(program.memoryPlan.pools.map((p) => p.id));
+  values.forEach((v, i) => {
+    if (v.type === 'tensor' && v.memObjId !== undefined && !poolIds.has(v.memObjId)) {
+      throw new Error(`values[${i}] has memObjId=${v.memObjId} but no matching pool in memoryPlan. ` +
+        `Available pools: [${[...poolIds].sort((a, b) => a - b).join(', ')}]`);
+    }
+  });
+  values.forEach((v, i) => {
+    if (v.type === 'tensor' && v.weightsOffset !== undefined) {
+      const end = v.weightsOffset + v.weightsLength;
+      if (end > weightsByteLength) {
+        throw new Error(`values[${i}] weights [${v.weightsOffset}:${end}] exceeds weights.bin size (${weightsByteLength})`);
+      }
     }
   });
 }
@@ -797,6 +856,6 @@ function fromFloat16Array(bits) {
 
 module.exports = {
   GPUBufferUsage, MAX_NDIM, DTYPE_BYTESIZE, Tensor, WgpuExecutionContext, WgxDevice, WgxBuffer,
-  requestDevice, createDevice, resolveArgs, shaders, shaderRegistry, toHalf, fromHalf,
+  requestDevice, createDevice, resolveArgs, validateProgram, shaders, shaderRegistry, toHalf, fromHalf,
   toFloat16Array, fromFloat16Array, _planViews: planViews,
 };

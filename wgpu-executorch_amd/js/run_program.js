@@ -19,7 +19,8 @@
  * --no-bind-io copies the input into and the output out of the memory plan
  * instead of binding the caller's tensors,
  * --eager replays the recorded launches one by one on the stream instead of
- * through a HIP graph.
+ * through a HIP graph.  The program is checked with the converter's rules
+ * (validateProgram) before it is recorded.
  */
 const fs = require('fs');
 const path = require('path');
@@ -52,6 +53,7 @@ async function main() {
   const weights = wbuf.buffer.slice(wbuf.byteOffset, wbuf.byteOffset + wbuf.byteLength);
   const ibuf = fs.readFileSync(path.join(args.dir, 'input.bin'));
 
+  W.validateProgram(program, weights.byteLength);
   const device = await W.requestDevice(args.device);
   const ctx = new W.WgpuExecutionContext(device);
   const inV = program.values[program.inputIds[0]];

@@ -164,6 +164,26 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
         throw new Error(`${name}: expected output spatial [${eoh}, ${eow}]`);
       }
     }
+    // The reference's generic im2col GEMM variant (dense, not 1x1, K not a
+    // multiple of 4 or fewer than 64 output pixels, or OC < 8) launches one
+    // workgroup per 32 x 32 tile and refuses grids past 65535 in either
+    // direction (src/shaders/convolution/index.ts:168-205, 278-286); the
+    // MI355X kernels have no such limit, but the drop-in keeps the refusal.
+    const [b] = inTensor.shape;
+    const oc = outTensor.shape[1];
+    const nPix = b * outTensor.shape[2] * outTensor.shape[3];
+    if (name === 'aten.convolution.default' && !transposed && groups === 1) {
+      const is1x1 = kh === 1 && kw === 1 && sH === 1 && sW === 1 && pH === 0 && pW === 0 && dH === 1 && dW === 1;
+      const is1x1Vec4 = is1x1 && ic % 4 === 0 && (outTensor.shape[2] * outTensor.shape[3]) % 4 === 0 && oc % 4 === 0;
+      const is1x1Tiled = is1x1Vec4 && b === 1 && outTensor.shape[2] * outTensor.shape[3] >= 64 && ic >= 16;
+      const isDenseTiled = oc >= 8 && nPix >= 64 && (ic * kh * kw) % 4 === 0;
+      const isF16 = inTensor.dtype === 'float16';
+      const isDepthwise = oc === 1 && ic === 1 && kh * kw <= 49 && b <= 65535;  // groups === oc === ic
+      const generic = !isDepthwise && !is1x1Tiled && !isDenseTiled && !(is1x1 && !isF16);
+      if (generic && (Math.ceil(nPix / 32) > 65535 || Math.ceil(oc / 32) > 65535)) {
+        throw new Error(`${name}: GEMM tile grid exceeds dispatch limit`);
+      }
+    }
     const hasClamp = clampMin !== undefined || clampMax !== undefined;
     native.recordConv2d(ctx._h, inTensor._c(), weight._c(), bias === undefined ? null : bias._c(), {
       stride: [sH, sW], padding: [pH, pW], dilation: [dH, dW], outputPadding: [opH, opW],
@@ -348,23 +368,82 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
     },
   };
 
+  // src/shaders/max-pool-2d/index.ts:41-106: values and int32 indices
   const maxPool2d = {
     name: 'aten.max_pool2d_with_indices.default',
-    code: { all: 'max-pool kernel (values)' },
+    code: { all: 'max-pool kernel (values and indices); chained same-size pools fold into one launch' },
     recordIn(ctx, [inTensor, kernelSize, stride, padding, dilation, ceilMode, outs]) {
       const name = 'aten.max_pool2d_with_indices.default';
-      const k = parseHw(name, kernelSize, 'kernel_size');
-      const s = stride.length === 0 ? k : parseHw(name, stride, 'stride');
-      const p = parseHw(name, padding, 'padding');
-      const d = parseHw(name, dilation, 'dilation');
-      if (outs.length < 1) throw new Error(`${name}: expected 2 outputs [values, indices], got ${outs.length}`);
-      const vals = outs[0];
+      if (outs.length !== 2) throw new Error(`${name}: expected 2 outputs [values, indices], got ${outs.length}`);
+      const [vals, idx] = outs;
       if (!isFloatPair(inTensor) || vals.dtype !== inTensor.dtype) {
         throw new Error(`${name}: values tensors must have matching float32 or float16 dtype`);
       }
+      if (idx.dtype !== 'int32') throw new Error(`${name}: indices output must be int32`);
       if (inTensor.shape.length !== 4) throw new Error(`${name}: input must be 4D NCHW`);
-      if (ceilMode) throw new Error(`${name}: ceil_mode is not supported`);
-      native.recordMaxPool2d(ctx._h, inTensor._c(), k, s, p, d, vals._c());
+      const [b, c, ih, iw] = inTensor.shape;
+      const [kH, kW] = parseHw(name, kernelSize, 'kernel_size');
+      const [sH, sW] = parseHw(name, stride, 'stride');
+      const [pH, pW] = parseHw(name, padding, 'padding');
+      const [dH, dW] = parseHw(name, dilation, 'dilation');
+      const ohNum = ih + 2 * pH - (dH * (kH - 1) + 1);
+      const owNum = iw + 2 * pW - (dW * (kW - 1) + 1);
+      const oh = Math.max(0, (ceilMode ? Math.ceil(ohNum / sH) : Math.floor(ohNum / sH)) + 1);
+      const ow = Math.max(0, (ceilMode ? Math.ceil(owNum / sW) : Math.floor(owNum / sW)) + 1);
+      const want = [b, c, oh, ow];
+      const same = (t) => t.shape.length === 4 && t.shape.every((v, i) => v === want[i]);
+      if (!same(vals)) throw new Error(`${name}: values output shape ${vals.shape} != [${want.join(', ')}]`);
+      if (!same(idx)) throw new Error(`${name}: indices output shape ${idx.shape} != [${want.join(', ')}]`);
+      native.recordMaxPool2d(ctx._h, inTensor._c(), [kH, kW], [sH, sW], [pH, pW], [dH, dW], ceilMode ? 1 : 0,
+        vals._c(), idx._c());
+    },
+  };
+
+  // src/shaders/permute/index.ts:33-99
+  const permuteCopy = {
+    name: 'aten.permute_copy.default',
+    code: { transpose: 'permute_transpose (64x64 LDS tiles, last two dims swapped)', other: 'permute_gather' },
+    recordIn(ctx, [inTensor, dims, outTensor]) {
+      const name = 'aten.permute_copy.default';
+      if (!isFloatPair(inTensor) || outTensor.dtype !== inTensor.dtype) {
+        throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+      }
+      const rank = inTensor.shape.length;
+      if (outTensor.shape.length !== rank) throw new Error(`${name}: output rank != input rank`);
+      if (dims.length !== rank) throw new Error(`${name}: dims count (${dims.length}) != input rank (${rank})`);
+      const perm = [];
+      const seen = new Set();
+      for (let d = 0; d < rank; d++) {
+        let p = dims[d];
+        if (p < 0) p += rank;
+        if (p < 0 || p >= rank || seen.has(p)) throw new Error(`${name}: invalid permute dims ${dims}`);
+        seen.add(p);
+        perm.push(p);
+      }
+      for (let d = 0; d < rank; d++) {
+        if (outTensor.shape[d] !== inTensor.shape[perm[d]]) {
+          throw new Error(`${name}: output shape does not match permuted input shape`);
+        }
+      }
+      native.recordPermute(ctx._h, inTensor._c(), perm, outTensor._c());
+    },
+  };
+
+  // src/shaders/softmax/index.ts:62-125
+  const softmax = {
+    name: 'aten._softmax.default',
+    code: { rows: 'softmax_rows (a wave per contiguous row)', other: 'softmax_strided' },
+    recordIn(ctx, [inTensor, dim, , outTensor]) {
+      const name = 'aten._softmax.default';
+      if (!isFloatPair(inTensor) || outTensor.dtype !== inTensor.dtype) {
+        throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
+      }
+      if (inTensor.shape.length === 0) throw new Error(`${name}: scalar input unsupported`);
+      if (inTensor.numel !== outTensor.numel) throw new Error(`${name}: input/output numel mismatch`);
+      const ndim = inTensor.shape.length;
+      const d = dim < 0 ? dim + ndim : dim;
+      if (d < 0 || d >= ndim) throw new Error(`${name}: dim out of range`);
+      native.recordSoftmax(ctx._h, inTensor._c(), d, outTensor._c());
     },
   };
 
@@ -385,7 +464,7 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
     add, sub, mul, sigmoid, relu, hardswish,
     mm, addmm, linear, bmm,
     convolution, convWithClamp, convolutionSilu, convolutionSiluAdd, maxPool2d,
-    upsampleNearest2d,
+    upsampleNearest2d, permuteCopy, softmax,
     cat, splitWithSizesCopy,
     viewCopy: flatCopy('aten.view_copy.default'),
     clone: flatCopy('aten.clone.default'),

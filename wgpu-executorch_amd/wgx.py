@@ -2,7 +2,7 @@
 
 Mirrors the reference's host API for the hot path with Python naming:
 ``Context`` is WgpuExecutionContext (src/context.ts:17-390), ``Tensor`` is the
-non-owning view of src/tensor.ts:77-192, and the ``record_*`` methods are the
+non-owning view of src/tensor.ts:43-159, and the ``record_*`` methods are the
 ``recordIn`` bodies of the Shader objects (src/shaders/mm/index.ts:32-93,
 src/shaders/bmm/index.ts:27-96, src/shaders/convolution/index.ts:58-310),
 plus ``addmm`` (absent from the reference).
@@ -96,9 +96,15 @@ SIGNATURES = {
     "wgx_record_upsample_nearest2d": (_I, [_P, _T, _T]),
     "wgx_record_max_pool2d": (_I, [_P, _T, ctypes.POINTER(ctypes.c_int32),
                                    ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
-                                   ctypes.POINTER(ctypes.c_int32), _T]),
+                                   ctypes.POINTER(ctypes.c_int32), _I, _T, _T]),
+    "wgx_record_permute": (_I, [_P, _T, ctypes.POINTER(ctypes.c_int32), _I, _T]),
+    "wgx_record_softmax": (_I, [_P, _T, _I, _T]),
     "wgx_submit": (_I, [_P]),
     "wgx_sync": (_I, [_P]),
+    "wgx_fence_record": (_I, [_P, ctypes.POINTER(_P)]),
+    "wgx_fence_wait": (_I, [_P]),
+    "wgx_fence_error": (ctypes.c_char_p, [_P]),
+    "wgx_fence_destroy": (None, [_P]),
     "wgx_reset": (_I, [_P]),
     "wgx_command_count": (_I, [_P]),
     "wgx_set_graph_mode": (_I, [_P, _I]),
@@ -360,12 +366,29 @@ class Context:
         self._check(lib().wgx_record_upsample_nearest2d(self.h, ctypes.byref(cx), ctypes.byref(co)))
         return self
 
-    def max_pool2d(self, x: Tensor, kernel, stride, padding, dilation, out: Tensor):
+    def max_pool2d(self, x: Tensor, kernel, stride, padding, dilation, out: Tensor,
+                   indices: Optional[Tensor] = None, ceil_mode: bool = False):
+        """max_pool2d_with_indices: values into out, int32 indices (if given)."""
         def arr(v):
             return (ctypes.c_int32 * 2)(*v)
         cx, co = x.c(), out.c()
+        ci = indices.c() if indices is not None else None
         self._check(lib().wgx_record_max_pool2d(self.h, ctypes.byref(cx), arr(kernel), arr(stride),
-                                                arr(padding), arr(dilation), ctypes.byref(co)))
+                                                arr(padding), arr(dilation), int(bool(ceil_mode)),
+                                                ctypes.byref(co),
+                                                ctypes.byref(ci) if ci is not None else None))
+        return self
+
+    def permute(self, x: Tensor, dims: Sequence[int], out: Tensor):
+        """permute_copy: out dim k is input dim dims[k]."""
+        cx, co = x.c(), out.c()
+        d = (ctypes.c_int32 * max(1, len(dims)))(*dims)
+        self._check(lib().wgx_record_permute(self.h, ctypes.byref(cx), d, len(dims), ctypes.byref(co)))
+        return self
+
+    def softmax(self, x: Tensor, dim: int, out: Tensor):
+        cx, co = x.c(), out.c()
+        self._check(lib().wgx_record_softmax(self.h, ctypes.byref(cx), int(dim), ctypes.byref(co)))
         return self
 
     # ------------------------------------------------------------ execution
@@ -374,6 +397,22 @@ class Context:
 
     def sync(self):
         self._check(lib().wgx_sync(self.h))
+
+    def fence(self) -> int:
+        """Marks the queue's current end; wait_fence(f) may run on any thread."""
+        f = ctypes.c_void_p()
+        self._check(lib().wgx_fence_record(self.h, ctypes.byref(f)))
+        return f.value or 0
+
+    @staticmethod
+    def wait_fence(f: int, destroy: bool = True):
+        try:
+            r = lib().wgx_fence_wait(f)
+            if r != 0:
+                raise WgxError(r, lib().wgx_fence_error(f).decode())
+        finally:
+            if destroy:
+                lib().wgx_fence_destroy(f)
 
     def reset(self):
         self._check(lib().wgx_reset(self.h))
