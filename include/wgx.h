@@ -155,6 +155,25 @@ int wgx_record_mm(wgx_ctx* ctx, const wgx_tensor* a, const wgx_tensor* b,
                   const wgx_tensor* bias, const wgx_tensor* out, float alpha, float beta,
                   uint32_t flags);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc): the wgx_record_mm GEMM (same arguments, same kernels,
+ * same results) launched at once on the context's stream instead of being
+ * recorded, with its workspace -- the [N, K] copy of a 16-bit [K, N] B that
+ * the large-tile kernel reads, and split-K partial sums -- taken from one
+ * fixed device array of WGX_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends.  It calls no hipMalloc / hipFree (nor any allocating
+ * routine); a GEMM whose workspace exceeds the array fails with
+ * WGX_ERR_INVALID before anything is launched.  Every call on a GPU shares
+ * that GPU's array: calls from contexts of one device are ordered on its
+ * single stream, but calls that overlap on one GPU from different device
+ * states (separately created contexts) race on it.  Host-only contexts fail
+ * with WGX_ERR_NO_DEVICE. */
+#define WGX_NOALLOC_SCRATCH_BYTES (8u << 20)
+int wgx_mm_noalloc(wgx_ctx* ctx, const wgx_tensor* a, const wgx_tensor* b,
+                   const wgx_tensor* bias, const wgx_tensor* out, float alpha, float beta,
+                   uint32_t flags);
+
 /* aten.bmm.default [a, b, out] (src/shaders/bmm/index.ts:27-96):
  * a [B,M,K] @ b [B,K,N] (or [B,N,K] with WGX_MM_TRANS_B) -> out [B,M,N]. */
 int wgx_record_bmm(wgx_ctx* ctx, const wgx_tensor* a, const wgx_tensor* b,

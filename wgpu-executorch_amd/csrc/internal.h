@@ -84,6 +84,9 @@ void conv_fill_ktab(uint32_t* tab, int K, int IC, const ConvGeom& g);
 bool conv_ktab_fits(int K, int IC, const ConvGeom& g);
 
 hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name);
+// Device address of the fixed WGX_NOALLOC_SCRATCH_BYTES workspace on
+// `device` (noalloc.hip), looked up once per device and cached.
+hipError_t noalloc_scratch(int device, void** out);
 hipError_t launch_gemm_f32(const GemmDesc& d, hipStream_t s, std::string* name);
 
 struct DwDesc {

@@ -263,6 +263,11 @@ int wgx_ctx_create(int device, wgx_ctx** out) {
       ds->arch = a.substr(0, a.find(':'));
     }
     ds->has_dev = true;
+    // the no-allocation entry point's scratch address, looked up once per
+    // device with the device current (a failure is kept and reported by
+    // wgx_mm_noalloc; nothing else depends on it)
+    void* scratch_ptr = nullptr;
+    noalloc_scratch(device, &scratch_ptr);
   }
   wgx_ctx* c = new wgx_ctx();
   c->d = ds;
@@ -438,9 +443,10 @@ static int record_gemm(wgx_ctx* c, GemmDesc d) {
   return c->push([d](hipStream_t s) { return launch_gemm_mfma(d, s, nullptr); }, name);
 }
 
-int wgx_record_mm(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* bias,
-                  const wgx_tensor* out, float alpha, float beta, uint32_t flags) {
-  CTX_GUARD(c);
+// Validates an mm / addmm and fills its GEMM description (shared by the
+// recorded and the no-allocation entry points).
+static int mm_desc(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* bias,
+                   const wgx_tensor* out, float alpha, float beta, uint32_t flags, GemmDesc* dp) {
   int r;
   if ((r = c->check(a, "mm: in1")) || (r = c->check(b, "mm: in2")) || (r = c->check(out, "mm: out")))
     return r;
@@ -484,7 +490,66 @@ int wgx_record_mm(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wg
     else return c->fail(WGX_ERR_INVALID, "addmm: bias must broadcast as [N], [1,N] or [M,1]");
     d.bias = bias->data;
   }
+  *dp = d;
+  return WGX_OK;
+}
+
+int wgx_record_mm(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* bias,
+                  const wgx_tensor* out, float alpha, float beta, uint32_t flags) {
+  CTX_GUARD(c);
+  GemmDesc d{};
+  if (int r = mm_desc(c, a, b, bias, out, alpha, beta, flags, &d)) return r;
   return record_gemm(c, d);
+}
+
+int wgx_mm_noalloc(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* bias,
+                   const wgx_tensor* out, float alpha, float beta, uint32_t flags) {
+  CTX_GUARD(c);
+  GemmDesc d{};
+  if (int r = mm_desc(c, a, b, bias, out, alpha, beta, flags, &d)) return r;
+  if (!c->d->has_dev) return c->fail(WGX_ERR_NO_DEVICE, "mm_noalloc: host-only context has no device");
+  // the same kernel choice as record_gemm, with the workspace carved out of
+  // the fixed per-device scratch array instead of context-owned memory
+  std::string name;
+  bool mfma = d.dtype != WGX_FLOAT32;
+  hipError_t e = hipSuccess;
+  d.splits = 1;
+  if (d.dtype == WGX_FLOAT32 && f32_on_mfma()) {
+    e = launch_gemm_mfma(d, describe_only(), &name);
+    if (e == hipSuccess) mfma = true;
+    else if (e != hipErrorNotSupported) return c->hip_fail(e, "mm_noalloc: kernel set-up");
+  }
+  if (mfma) {
+    size_t ws_bytes = 0;
+    const int splits = gemm_split_plan(d, &ws_bytes);
+    const size_t bt_bytes = gemm_stage_b_bytes(d);
+    const size_t ws_span = (ws_bytes + 255) / 256 * 256;
+    if (ws_span + bt_bytes > WGX_NOALLOC_SCRATCH_BYTES)
+      return c->fail(WGX_ERR_INVALID,
+                     "mm_noalloc: this GEMM needs %llu bytes of workspace; the fixed scratch holds %u",
+                     (unsigned long long)(ws_span + bt_bytes), (unsigned)WGX_NOALLOC_SCRATCH_BYTES);
+    if (ws_span + bt_bytes > 0) {
+      void* base = nullptr;
+      e = noalloc_scratch(c->d->device, &base);
+      if (e != hipSuccess) return c->hip_fail(e, "mm_noalloc: scratch address");
+      // every split-K range writes all of its partial sums and the staging
+      // pass writes the whole [N, K] copy before they are read, so nothing
+      // left by an earlier call is ever read and nothing needs clearing
+      if (splits > 1) {
+        d.splits = splits;
+        d.ws = static_cast<float*>(base);
+      }
+      if (bt_bytes > 0) d.bt = static_cast<char*>(base) + ws_span;
+    }
+    e = launch_gemm_mfma(d, describe_only(), &name);  // one-time kernel set-up (LDS limits)
+    if (e == hipSuccess) e = launch_gemm_mfma(d, c->d->stream, nullptr);
+  } else {
+    e = launch_gemm_f32(d, describe_only(), &name);
+    if (e == hipSuccess) e = launch_gemm_f32(d, c->d->stream, nullptr);
+  }
+  if (e != hipSuccess) return c->hip_fail(e, "mm_noalloc");
+  c->last_kernel = name;
+  return WGX_OK;
 }
 
 int wgx_record_bmm(wgx_ctx* c, const wgx_tensor* a, const wgx_tensor* b, const wgx_tensor* out,

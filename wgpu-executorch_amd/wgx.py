@@ -84,6 +84,7 @@ SIGNATURES = {
     "wgx_read": (_I, [_P, _P, _P, _U64]),
     "wgx_record_copy": (_I, [_P, _P, _P, _U64]),
     "wgx_record_mm": (_I, [_P, _T, _T, _T, _T, ctypes.c_float, ctypes.c_float, ctypes.c_uint32]),
+    "wgx_mm_noalloc": (_I, [_P, _T, _T, _T, _T, ctypes.c_float, ctypes.c_float, ctypes.c_uint32]),
     "wgx_record_bmm": (_I, [_P, _T, _T, _T, ctypes.c_uint32]),
     "wgx_record_conv2d": (_I, [_P, _T, _T, _T, ctypes.POINTER(CConvArgs), _T]),
     "wgx_record_conv2d_residual": (_I, [_P, _T, _T, _T, ctypes.POINTER(CConvArgs), _T, ctypes.c_float,
@@ -282,6 +283,18 @@ class Context:
                                         ctypes.byref(cb) if cb is not None else None,
                                         ctypes.byref(ct[2]), alpha, beta,
                                         MM_TRANS_B if trans_b else 0))
+        return self
+
+    def mm_noalloc(self, a: Tensor, b: Tensor, out: Tensor, bias: Optional[Tensor] = None,
+                   alpha: float = 1.0, beta: float = 1.0, trans_b: bool = False) -> "Context":
+        """The mm / addmm launched now on the context's stream, its workspace in
+        the library's fixed per-device scratch (no device allocation)."""
+        ct = [a.c(), b.c(), out.c()]
+        cb = bias.c() if bias is not None else None
+        self._check(lib().wgx_mm_noalloc(self.h, ctypes.byref(ct[0]), ctypes.byref(ct[1]),
+                                         ctypes.byref(cb) if cb is not None else None,
+                                         ctypes.byref(ct[2]), alpha, beta,
+                                         MM_TRANS_B if trans_b else 0))
         return self
 
     def addmm(self, bias: Tensor, x: Tensor, w: Tensor, out: Tensor, beta: float = 1.0,
