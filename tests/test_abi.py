@@ -122,6 +122,20 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
         hctx.convolution(x, w, b, stride, pad, dil, transposed, op, groups, y)
         return hctx.last_kernel
 
+    # dense 3x3 over a multiple of 16 channels: the LDS-patch kernel at batch
+    # 1 (32 x 64 tiles, 64 x 32 for 16-bit data at stride 2, W waves up to
+    # the 16-channel chunk count), 64 x 64 one-wave tiles for batched float32,
+    # and the GEMM kernels for batched 16-bit data
+    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)) == "conv_lds_f16_3x3s1_32x64w4"
+    assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "conv_lds_f16_3x3s2_64x32w8"
+    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="float32") == "conv_lds_f32_3x3s1_32x64w4"
+    assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1), dtype="float32") == "conv_lds_f32_3x3s2_32x64w8"
+    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="bfloat16") == "conv_lds_bf16_3x3s1_32x64w4"
+    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1), dtype="float32") == "conv_lds_f32_3x3s1_64x64w1"
+    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)).startswith("gemm_mfma_f16")
+    monkeypatch.setenv("WGX_CONV_LDS", "2x1w2")
+    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_lds_f16_3x3s1_64x32w2"
+    monkeypatch.setenv("WGX_CONV_LDS", "off")
     # fewer 64 x 64 tiles than CUs: the wave-split kernel, 64 x 32 tiles with
     # 4 waves (400 of them) or 8 waves (200)
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)) == "gemm_mfma_f16_64x32w4_conv_ws"
@@ -183,8 +197,9 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
         conv([1, 2, 3, 3], [2, 2, 3, 3], [1, 2, 7, 7], (2, 2), (1, 1), transposed=True, op=(2, 2))
     with pytest.raises(E, match="4D"):
         conv([1, 4, 8], [8, 4, 3, 3], [1, 8, 6, 6])
-    with pytest.raises(E, match="matching float32 or float16"):
-        conv([1, 4, 8, 8], [8, 4, 3, 3], [1, 8, 6, 6], dtype="bfloat16")
+    with pytest.raises(E, match="matching float32, float16 or bfloat16"):
+        hctx.convolution(T("bfloat16", [1, 4, 8, 8]), T("float16", [8, 4, 3, 3]), None, (1, 1), (0, 0),
+                         (1, 1), False, (0, 0), 1, T("bfloat16", [1, 8, 6, 6]))
 
 
 def test_im2col_table_matches_oracle_indexing(pkg, orc):

@@ -46,7 +46,7 @@ def test_reference_kats_conv(gpu_ctx, kats):
             assert abs(got.ravel()[0] - e0) <= c["tol"], c["source"]
 
 
-@pytest.mark.parametrize("dtype", ["float32", "float16"])
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
 @pytest.mark.parametrize("variant", ["2a", "2b"])
 def test_config2_conv(gpu_ctx, orc, pkg, dtype, variant):
     I = pkg.inputs
@@ -334,6 +334,7 @@ def test_wave_split_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg):
     """Every instantiated wave-split configuration (forced through WGX_WS)
     against the float64 convolution, including batch 2 and ragged tiles."""
     monkeypatch.setenv("WGX_WS", cfg)
+    monkeypatch.setenv("WGX_CONV_LDS", "off")  # the 3x3 cases would take the LDS-patch kernel
     I = pkg.inputs
     for i, (xs, ws, s, p, d) in enumerate(WS_CASES):
         x = round_in(I.uniform(800 + i, xs, -1, 1), dtype)
@@ -382,3 +383,57 @@ def test_depthwise_silu_residual_epilogue(gpu_ctx, orc, pkg, dtype):
         bound = 1.1 * abs(cs) * refa + abs(rs) * np.abs(r.astype(np.float64))
         assert_parity(ty.get_f32(), want, bound, dtype, ws[1] * ws[2] * ws[3],
                       f"residual {i} {dtype} {xs}x{ws} {kernel}")
+
+
+LDS_CASES = [
+    # x shape, w shape, stride, pad: ragged output channels, widths that are
+    # not a multiple of the 8-pixel region, batch 2, stride 2, padding 0 and 2,
+    # and maps smaller than one region
+    ((1, 16, 21, 13), (24, 16, 3, 3), 1, 1),
+    ((2, 32, 15, 17), (40, 32, 3, 3), 1, 1),
+    ((1, 64, 20, 20), (64, 64, 3, 3), 1, 1),
+    ((1, 128, 10, 10), (100, 128, 3, 3), 2, 1),
+    ((2, 48, 33, 31), (72, 48, 3, 3), 2, 1),
+    ((1, 16, 9, 9), (16, 16, 3, 3), 1, 0),
+    ((1, 32, 12, 11), (8, 32, 3, 3), 2, 2),
+    ((1, 16, 3, 5), (33, 16, 3, 3), 1, 1),
+]
+LDS_CONFIGS = ["2x2w1", "2x2w4", "2x1w2", "1x2w8", "2x1w1"]
+
+
+@pytest.mark.parametrize("cfg", LDS_CONFIGS)
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_lds_patch_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg):
+    """Every configuration of the LDS-patch 3x3 kernel (forced through
+    WGX_CONV_LDS) against the float64 convolution; every second case with a
+    bias, with SiLU or with a clamp in the epilogue."""
+    W = pkg.wgx
+    monkeypatch.setenv("WGX_CONV_LDS", cfg)
+    I = pkg.inputs
+    for i, (xs, ws, s, p) in enumerate(LDS_CASES):
+        x = round_in(I.uniform(900 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(910 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(920 + i, (ws[0],), -0.5, 0.5), dtype) if i % 2 else None
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), 1)
+        tx, tw = gpu_ctx.from_numpy(x, dtype), gpu_ctx.from_numpy(w, dtype)
+        tb = gpu_ctx.from_numpy(b, dtype) if b is not None else None
+        ty = gpu_ctx.tensor(dtype, list(ref.shape))
+        mode = i % 3  # 0 plain, 1 SiLU, 2 clamp
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], 1, ty,
+                            clamp=(-0.25, 0.5) if mode == 2 else None,
+                            activation=W.ACT_SILU if mode == 1 else W.ACT_NONE)
+        kernel = gpu_ctx.last_kernel
+        assert kernel.startswith("conv_lds_") and kernel.endswith(
+            f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}"), kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        got = ty.get_f32()
+        if mode == 1:
+            # the reference applies SiLU to the rounded-in-fp64 conv output; the
+            # bound carries the conv's error through SiLU (|d silu| <= 1.1)
+            ref = ref / (1.0 + np.exp(-ref))
+            refa = 1.1 * refa
+        elif mode == 2:
+            ref = np.clip(ref, -0.25, 0.5)
+        assert_parity(got, ref, refa, dtype, ws[1] * 9, f"lds {cfg} case {i} {dtype} {xs}x{ws} s{s} p{p} {kernel}")

@@ -1,0 +1,560 @@
+// conv_lds.hip -- dense KxK convolution (groups 1, dilation 1, input channels
+// a multiple of 16) as an implicit GEMM on the gfx950 matrix cores, with each
+// wave's input patch in LDS and no per-element address arithmetic.
+//
+// Serves the dense branch of aten.convolution / et_vk.conv_with_clamp
+// (src/shaders/convolution/index.ts:168-238: the tile64 / tile32 / gemm
+// implicit-im2col variants; conv-with-clamp/index.ts:60-319) for float16,
+// bfloat16 and float32 NCHW tensors with OIHW weights:
+//   y[b,oc,oh,ow] = bias[oc] + sum_{ic,kh,kw} w[oc,ic,kh,kw] * x[b,ic,oh*s-p+kh,ow*s-p+kw]
+// (zero outside the image), fp32 accumulation, then SiLU / clamp, one rounding.
+//
+// GEMM view: M = OC (the A operand, weight rows), N = output pixels (B, the
+// im2col columns), K = IC*KH*KW.  Each wave owns TM x TN MFMA tiles of 32 x 32:
+// TM*32 output channels by a region of 4*TN x 8 output pixels (each 32-pixel
+// MFMA column block is a 4 x 8 rectangle, so a region's input footprint is a
+// small 2-D patch rather than a row strip).
+//
+// K is walked in chunks of 16 input channels.  Within a chunk the K order is
+// arranged so that both operands need no address work:
+//   * lanes 0-31 take the chunk's channels 0-7 and lanes 32-63 channels 8-15;
+//     each lane half walks its 8 channels x T taps (T = KH*KW) in the
+//     natural (ic, kh, kw) order, 16 bytes at a time;
+//   * A: those 8T k of a weight row are contiguous in OIHW memory, so every
+//     A fragment is ONE 16-byte buffer load at a loop-invariant lane offset
+//     plus a compile-time step offset;
+//   * B: the chunk's input patch (16 channels x PH x PW, zero outside the
+//     image) sits in the wave's own LDS; the element a lane needs for k =
+//     (channel, kh, kw) of its output pixel is at
+//         pixel_base(lane) + (channel * PH * PW + kh * PW + kw) * ES
+//     where the second term is a compile-time constant per (step, element):
+//     one ds_read with an immediate offset per element.
+// Both operands see the same k order, so the GEMM computes the convolution.
+// The patch of the next chunk is loaded (lane-strided, one buffer load per
+// element at precomputed lane offsets, the chunk selected by the descriptor
+// base) while the current chunk is multiplied.  Each wave has its own patch,
+// so the K loop has no barrier.
+//
+// Few output tiles (batch-1 maps): the W waves of a block share one tile and
+// take chunks w, w+W, ...; their partial sums meet in LDS and are added in
+// wave order (fixed, so the result does not depend on timing).
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "internal.h"
+
+namespace wgx {
+namespace {
+
+using f32x16 = float __attribute__((ext_vector_type(16)));
+using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
+using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr uint32_t OOB = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+// The scalar offset (soff) is added to the lane's offset by the load itself:
+// per-element constants cost no vector instruction.
+__device__ __forceinline__ uint4 ld16(rsrc_t r, uint32_t off, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+template <int ES>
+__device__ __forceinline__ uint32_t ld_el(rsrc_t r, uint32_t off, uint32_t soff) {
+  if constexpr (ES == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, (int)soff, 0);
+  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, (int)soff, 0);
+}
+
+struct CParams {
+  const void* x;
+  const void* w;
+  const void* bias;
+  void* y;
+  int IC, IH, IW, OC, OH, OW, pH, pW;
+  long long sx, sy;  // elements per input / output image
+  int tiles_m, tiles_w, tiles_h, ntiles;
+  int nchunks;  // IC / 16
+  int W;        // waves per block sharing one tile
+  int act, has_clamp;
+  float cmin, cmax;
+};
+
+template <int DT>
+__device__ __forceinline__ f32x16 mma(uint4 b, uint4 a, f32x16 c) {
+  if constexpr (DT == WGX_FLOAT32) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(b.x), __uint_as_float(a.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(b.y), __uint_as_float(a.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(b.z), __uint_as_float(a.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(b.w), __uint_as_float(a.w), c, 0, 0, 0);
+    return c;
+  } else if constexpr (DT == WGX_BFLOAT16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b), __builtin_bit_cast(bf16x8, a),
+                                                   c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c,
+                                                  0, 0, 0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float to_f(uint32_t h) {
+  if constexpr (DT == WGX_FLOAT32) return __uint_as_float(h);
+  else if constexpr (DT == WGX_BFLOAT16) return __uint_as_float(h << 16);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t from_f(float v) {
+  if constexpr (DT == WGX_FLOAT32) return __float_as_uint(v);
+  else if constexpr (DT == WGX_BFLOAT16) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  } else {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+  }
+}
+
+// Geometry of one wave's region and its patch.  In LDS a channel's patch
+// plane (PH x PW, row-major) is padded to whole blocks of 64 elements: patch
+// element (channel, block, lane) sits at (channel * PHWP + block * 64 + lane),
+// so each lane's load targets for every channel differ only by constants.
+template <int DT, int KH, int KW, int S, int TN>
+struct Geo {
+  static constexpr int ES = DT == WGX_FLOAT32 ? 4 : 2;
+  static constexpr int EPC = 16 / ES;            // k per lane per 16-byte fragment
+  static constexpr int T = KH * KW;
+  static constexpr int STEPS = 8 * T / EPC;      // fragments per chunk per lane half
+  static constexpr int RH = 4 * TN, RW = 8;      // output pixels of the region
+  static constexpr int PH = (RH - 1) * S + KH;   // input rows / columns it reads
+  static constexpr int PW = (RW - 1) * S + KW;
+  static constexpr int PHW = PH * PW;
+  static constexpr int NBLK = (PHW + 63) / 64;   // 64-element blocks per channel plane
+  static constexpr int PHWP = NBLK * 64;         // padded plane
+  static constexpr int LDS_WAVE = 16 * PHWP * ES;  // bytes of a wave's patch
+  // A fragments kept in flight ahead of the one being multiplied
+  static constexpr int PF = ES == 4 ? STEPS / 3 : STEPS;
+  static_assert(STEPS % PF == 0, "the prefetch ring wraps at chunk ends");
+  // LDS byte offset, relative to the lane's pixel base, of element e of
+  // fragment step s (lane half channel = k / T, tap = k % T, k = s*EPC + e)
+  static constexpr int boff(int s, int e) {
+    const int k = s * EPC + e, ch = k / T, tap = k % T;
+    return (ch * PHWP + (tap / KW) * PW + (tap % KW)) * ES;
+  }
+};
+
+template <int DT, int KH, int KW, int S, int TM, int TN>
+__global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
+  using G = Geo<DT, KH, KW, S, TN>;
+  constexpr int ES = G::ES, T = G::T, STEPS = G::STEPS, NBLK = G::NBLK, PF = G::PF;
+  constexpr int NG = TM * TN * 4;  // accumulator groups of 4 per lane
+  extern __shared__ uint4 lds_u4[];
+  char* lds = reinterpret_cast<char*>(lds_u4);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = p.W;
+  const int fr = lane & 31, fc = lane >> 5;
+  // XCD-aware numbering (block ids are dealt round-robin to the 8 XCDs):
+  // XCD x gets a contiguous run of tiles; output-channel tiles vary fastest,
+  // so the tiles of one pixel region (one input patch) meet in one L2
+  const int Gn = gridDim.x;
+  const int rb = (Gn & 7) == 0 ? (blockIdx.x & 7) * (Gn >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  int t = rb;
+  const int tm = t % p.tiles_m;
+  t /= p.tiles_m;
+  const int tw = t % p.tiles_w;
+  t /= p.tiles_w;
+  const int th = t % p.tiles_h;
+  const int z = t / p.tiles_h;
+  const int m0 = tm * TM * 32, oh0 = th * G::RH, ow0 = tw * G::RW;
+  const int K = p.IC * T;
+
+  // A: lane offset of its weight row's 16-byte run (this lane half's 8
+  // channels of the chunk); rows past OC read zero
+  uint32_t va[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int oc = m0 + i * 32 + fr;
+    va[i] = oc < p.OC ? (uint32_t)(oc * K + fc * 8 * T) * ES : OOB;
+  }
+  // patch block e of a channel: this lane's (row, column) of the patch
+  // and its input offset in channel 0 of the chunk (OOB outside the image or
+  // past the plane)
+  const int ih0 = oh0 * S - p.pH, iw0 = ow0 * S - p.pW;
+  const int plane = p.IH * p.IW;
+  uint32_t vp[NBLK];
+#pragma unroll
+  for (int e = 0; e < NBLK; ++e) {
+    const int q = e * 64 + lane;
+    const int pr = q / G::PW, pc = q - pr * G::PW;
+    const int ih = ih0 + pr, iw = iw0 + pc;
+    vp[e] = (q < G::PHW && ih >= 0 && ih < p.IH && iw >= 0 && iw < p.IW) ? (uint32_t)(ih * p.IW + iw) * ES : OOB;
+  }
+  char* wl = lds + wave * G::LDS_WAVE;
+  // B: the lane's output pixel in each 4 x 8 block of the region
+  // the lane's bias per row block, fetched now, off the epilogue's path
+  float brow[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int oc = m0 + i * 32 + fr;
+    brow[i] = (p.bias && oc < p.OC)
+                  ? to_f<DT>(ES == 4 ? reinterpret_cast<const uint32_t*>(p.bias)[oc]
+                                     : (uint32_t)reinterpret_cast<const uint16_t*>(p.bias)[oc])
+                  : 0.0f;
+  }
+  int vb[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+    vb[j] = (fc * 8 * G::PHWP + ((4 * j + (fr >> 3)) * S) * G::PW + (fr & 7) * S) * ES;
+
+  const char* ximg = static_cast<const char*>(p.x) + (long long)z * p.sx * ES;
+  const char* wbase = static_cast<const char*>(p.w);
+  const uint32_t chunk_x = (uint32_t)(16 * plane * ES), chunk_w = (uint32_t)(16 * T * ES);
+  const uint32_t wbytes = (uint32_t)((long long)p.OC * K * ES);
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // the chunk's patch in registers: 16 channels x NBLK blocks (16-bit
+  // elements two channels to a register)
+  constexpr int NPV = ES == 4 ? 16 * NBLK : 8 * NBLK;
+  uint32_t pv[NPV];
+  const uint32_t cplane = (uint32_t)(plane * ES);
+  auto load_patch = [&](int c) {
+    const rsrc_t rx = rsrc(ximg + (long long)c * chunk_x, chunk_x);
+#pragma unroll
+    for (int e = 0; e < NBLK; ++e)
+#pragma unroll
+      for (int ch = 0; ch < 16; ch += (ES == 4 ? 1 : 2)) {
+        if constexpr (ES == 4) {
+          pv[ch * NBLK + e] = ld_el<4>(rx, vp[e], ch * cplane);
+        } else {
+          const uint32_t lo = ld_el<2>(rx, vp[e], ch * cplane), hi = ld_el<2>(rx, vp[e], (ch + 1) * cplane);
+          pv[(ch >> 1) * NBLK + e] = lo | (hi << 16);
+        }
+      }
+  };
+  auto store_patch = [&]() {
+#pragma unroll
+    for (int e = 0; e < NBLK; ++e)
+#pragma unroll
+      for (int ch = 0; ch < 16; ++ch) {
+        char* dst = wl + (ch * G::PHWP + e * 64 + lane) * ES;
+        if constexpr (ES == 4) *reinterpret_cast<uint32_t*>(dst) = pv[ch * NBLK + e];
+        else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(pv[(ch >> 1) * NBLK + e] >> (16 * (ch & 1)));
+      }
+  };
+
+  // A fragments run PF steps ahead of the multiply, across chunk ends: a[s %
+  // PF] holds step s of the current chunk, and once it is consumed the slot
+  // takes step s + PF (of this chunk, or of the wave's next chunk)
+  auto wrsrc = [&](int cc) { return rsrc(wbase + (long long)cc * chunk_w, wbytes - (uint32_t)cc * chunk_w); };
+  uint4 a[PF][TM];
+  int c = wave;
+  if (c < p.nchunks) {
+    load_patch(c);
+    const rsrc_t rw0 = wrsrc(c);
+#pragma unroll
+    for (int s = 0; s < PF; ++s)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[s][i] = ld16(rw0, va[i], (uint32_t)(s * 16));
+  }
+  for (; c < p.nchunks; c += W) {
+    const bool more = c + W < p.nchunks;
+    const rsrc_t rw = wrsrc(c);
+    const rsrc_t rn = wrsrc(more ? c + W : c);
+    // the patch -> LDS (the previous chunk's reads came first: a wave's LDS
+    // operations run in order)
+    store_patch();
+    asm volatile("" ::: "memory");
+    if (more) load_patch(c + W);
+    // B fragments of step s + 1 are read from LDS while step s multiplies
+    // (two register sets; the scheduling barriers keep the compiler from
+    // sinking the reads next to their first use)
+    auto read_b = [&](uint4* bf, int s) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const char* pb = wl + vb[j];
+        if constexpr (ES == 4) {
+          bf[j].x = *reinterpret_cast<const uint32_t*>(pb + G::boff(s, 0));
+          bf[j].y = *reinterpret_cast<const uint32_t*>(pb + G::boff(s, 1));
+          bf[j].z = *reinterpret_cast<const uint32_t*>(pb + G::boff(s, 2));
+          bf[j].w = *reinterpret_cast<const uint32_t*>(pb + G::boff(s, 3));
+        } else {
+          const uint32_t h0 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 0));
+          const uint32_t h1 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 1));
+          const uint32_t h2 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 2));
+          const uint32_t h3 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 3));
+          const uint32_t h4 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 4));
+          const uint32_t h5 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 5));
+          const uint32_t h6 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 6));
+          const uint32_t h7 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 7));
+          bf[j] = make_uint4(h0 | (h1 << 16), h2 | (h3 << 16), h4 | (h5 << 16), h6 | (h7 << 16));
+        }
+      }
+    };
+    uint4 bb[2][TN];
+    read_b(bb[0], 0);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      uint4 af[TM];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = a[s % PF][i];
+      if (s + PF < STEPS) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[s % PF][i] = ld16(rw, va[i], (uint32_t)((s + PF) * 16));
+      } else if (more) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[s % PF][i] = ld16(rn, va[i], (uint32_t)((s + PF - STEPS) * 16));
+      }
+      if (s + 1 < STEPS) read_b(bb[(s + 1) & 1], s + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint4* b = bb[s & 1];
+      if constexpr (ES == 4) {
+        // the four k of a fragment, each over every accumulator in turn, so
+        // consecutive MFMAs never wait on each other's results
+        const float* bf = reinterpret_cast<const float*>(b);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j * 4 + e],
+                                                              __uint_as_float(reinterpret_cast<const uint32_t*>(&af[i])[e]),
+                                                              acc[i][j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int i = 0; i < TM; ++i) acc[i][j] = mma<DT>(b[j], af[i], acc[i][j]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("" ::: "memory");
+  }
+
+  // ------------------------------------------------ epilogue
+  // acc[i][j][4g + e]: output channel m0 + i*32 + fr, region row 4j + g,
+  // region column 4fc + e
+  float* part = reinterpret_cast<float*>(lds);
+  if (W > 1) {
+    __syncthreads();  // every wave is done with its patch
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          reinterpret_cast<float4*>(part)[(wave * NG + (i * TN + j) * 4 + g) * 64 + lane] =
+              make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+    __syncthreads();
+  }
+  const bool vec = (p.OW & 3) == 0;
+  char* yimg = static_cast<char*>(p.y) + (long long)z * p.sy * ES;
+  auto store_group = [&](int q, float4 v) {
+    const int i = q / (TN * 4), j = (q >> 2) % TN, g = q & 3;
+    const int oc = m0 + i * 32 + fr, oh = oh0 + 4 * j + g, ow = ow0 + 4 * fc;
+    if (oc >= p.OC || oh >= p.OH || ow >= p.OW) return;
+    float bias = 0.0f;
+#pragma unroll
+    for (int ii = 0; ii < TM; ++ii)
+      if (ii == i) bias = brow[ii];
+    float vv[4] = {v.x + bias, v.y + bias, v.z + bias, v.w + bias};
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = apply_act(p.act, vv[e]);
+      if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+      h[e] = from_f<DT>(x);
+    }
+    char* dst = yimg + ((long long)oc * p.OH * p.OW + (long long)oh * p.OW + ow) * ES;
+    if (vec && ow + 3 < p.OW) {
+      if constexpr (ES == 4) *reinterpret_cast<uint4*>(dst) = make_uint4(h[0], h[1], h[2], h[3]);
+      else *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (ow + e < p.OW) {
+          if constexpr (ES == 4) reinterpret_cast<uint32_t*>(dst)[e] = h[e];
+          else reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)h[e];
+        }
+    }
+  };
+  if (W == 1) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          store_group((i * TN + j) * 4 + g,
+                      make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]));
+  } else {
+    for (int q = wave; q < NG; q += W) {
+      float4 v = reinterpret_cast<const float4*>(part)[q * 64 + lane];
+      for (int w = 1; w < W; ++w) {
+        const float4 u = reinterpret_cast<const float4*>(part)[(w * NG + q) * 64 + lane];
+        v.x += u.x;
+        v.y += u.y;
+        v.z += u.z;
+        v.w += u.w;
+      }
+      store_group(q, v);
+    }
+  }
+}
+
+struct Cfg {
+  int tm, tn, w;
+};
+
+template <int DT, int KH, int KW, int S, int TM, int TN>
+hipError_t launch_t(const CParams& p, size_t lds, unsigned grid, int w, hipStream_t s) {
+  auto fn = k_conv_lds<DT, KH, KW, S, TM, TN>;
+  static bool attr_set = false;
+  if (!attr_set && s != name_only()) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  if (is_dry(s)) return hipSuccess;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * w), lds, s, p);
+  return hipGetLastError();
+}
+
+template <int DT, int KH, int KW, int S, int TM, int TN>
+hipError_t launch_cfg(const CParams& p, const Cfg& c, unsigned grid, hipStream_t s) {
+  using G = Geo<DT, KH, KW, S, TN>;
+  const size_t patch = (size_t)c.w * G::LDS_WAVE;
+  const size_t part = c.w > 1 ? (size_t)c.w * TM * TN * 4 * 64 * 16 : 0;
+  const size_t lds = patch > part ? patch : part;
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  return launch_t<DT, KH, KW, S, TM, TN>(p, lds, grid, c.w, s);
+}
+
+// Instantiated tiles (TM x TN): 32 x 32 up to 64 x 128 (stride 1) and 64 x
+// 64 (stride 2, whose patches are four times larger).
+template <int DT, int KH, int KW, int S>
+hipError_t launch_geo(const CParams& p, const Cfg& c, unsigned grid, hipStream_t s) {
+  if (c.tm == 1 && c.tn == 1) return launch_cfg<DT, KH, KW, S, 1, 1>(p, c, grid, s);
+  if (c.tm == 1 && c.tn == 2) return launch_cfg<DT, KH, KW, S, 1, 2>(p, c, grid, s);
+  if (c.tm == 2 && c.tn == 1) return launch_cfg<DT, KH, KW, S, 2, 1>(p, c, grid, s);
+  if (c.tm == 2 && c.tn == 2) return launch_cfg<DT, KH, KW, S, 2, 2>(p, c, grid, s);
+  if constexpr (S == 1)
+    if (c.tm == 2 && c.tn == 4) return launch_cfg<DT, KH, KW, S, 2, 4>(p, c, grid, s);
+  return hipErrorInvalidValue;
+}
+
+long long tile_count(const ConvLdsDesc& d, const Cfg& c) {
+  return (long long)d.B * ((d.OC + 32 * c.tm - 1) / (32 * c.tm)) * ((d.OH + 4 * c.tn - 1) / (4 * c.tn)) *
+         ((d.OW + 7) / 8);
+}
+
+// The configuration for a shape, from sweeps of the 3x3 maps [1,64,80,80] ->
+// 128 (stride 1) and [1,128,80,80] -> 256 (stride 2) at batch 1 and 64:
+//  - few output tiles (under two per SIMD at 64 x 64: batch-1 maps): a 32 x
+//    64 tile (64 x 32 for 16-bit data at stride 2, whose patch is larger) and
+//    W waves per block splitting its 16-channel chunks, W up to the chunk
+//    count and 8 while the waves stay below four per SIMD;
+//  - many tiles: 64 x 64, one wave per tile, float32 only.  For 16-bit data
+//    the LDS-staged GEMM (gemm_mfma's 128 x 256 conv form) is faster there,
+//    and choose() returns tm = 0: the kernel does not apply.
+// WGX_CONV_LDS=TMxTNwW forces a configuration.
+Cfg choose(const ConvLdsDesc& d, int cus) {
+  const int chunks = d.IC / 16;
+  const long long simds = 4LL * cus;
+  Cfg c{2, 2, 1};
+  if (tile_count(d, c) < 2 * simds) {
+    if (d.dtype != WGX_FLOAT32 && d.sH == 2) c = Cfg{2, 1, 1};
+    else c = Cfg{1, 2, 1};
+    const long long tiles = tile_count(d, c);
+    int w = 1;
+    while (w < 8 && w * 2 <= chunks && tiles * w * 2 <= 4 * simds) w *= 2;
+    c.w = w;
+  } else if (d.dtype != WGX_FLOAT32) {
+    c.tm = 0;
+  }
+  if (const char* e = getenv("WGX_CONV_LDS")) {
+    int tm = 0, tn = 0, ww = 0;
+    if (sscanf(e, "%dx%dw%d", &tm, &tn, &ww) == 3 && tm >= 1 && tm <= 2 && tn >= 1 && tn <= 4 && ww >= 1 && ww <= 8)
+      c = Cfg{tm, tn, ww};
+  }
+  return c;
+}
+
+}  // namespace
+
+bool conv_lds_applies(const ConvLdsDesc& d) {
+  if (getenv("WGX_CONV_LDS") && strcmp(getenv("WGX_CONV_LDS"), "off") == 0) return false;
+  if (d.dtype != WGX_FLOAT16 && d.dtype != WGX_FLOAT32 && d.dtype != WGX_BFLOAT16) return false;
+  if (d.IC % 16 != 0 || d.IC <= 0 || d.OC <= 0) return false;
+  const bool geo = (d.KH == 3 && d.KW == 3 && d.sH == d.sW && (d.sH == 1 || d.sH == 2));
+  if (!geo) return false;
+  const int es = d.dtype == WGX_FLOAT32 ? 4 : 2;
+  // 32-bit buffer offsets: one input image and the whole weight tensor
+  if ((long long)d.IC * d.IH * d.IW * es >= (1LL << 31)) return false;
+  if ((long long)d.OC * d.IC * d.KH * d.KW * es >= (1LL << 31)) return false;
+  return true;
+}
+
+hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name) {
+  if (!conv_lds_applies(d)) return hipErrorNotSupported;
+  const Cfg c = choose(d, cus);
+  if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
+  CParams p{};
+  p.x = d.x;
+  p.w = d.w;
+  p.bias = d.bias;
+  p.y = d.y;
+  p.IC = d.IC;
+  p.IH = d.IH;
+  p.IW = d.IW;
+  p.OC = d.OC;
+  p.OH = d.OH;
+  p.OW = d.OW;
+  p.pH = d.pH;
+  p.pW = d.pW;
+  p.sx = (long long)d.IC * d.IH * d.IW;
+  p.sy = (long long)d.OC * d.OH * d.OW;
+  p.tiles_m = (d.OC + 32 * c.tm - 1) / (32 * c.tm);
+  p.tiles_h = (d.OH + 4 * c.tn - 1) / (4 * c.tn);
+  p.tiles_w = (d.OW + 7) / 8;
+  p.ntiles = d.B * p.tiles_m * p.tiles_h * p.tiles_w;
+  p.nchunks = d.IC / 16;
+  p.W = c.w;
+  p.act = d.act;
+  p.has_clamp = d.has_clamp;
+  p.cmin = d.cmin;
+  p.cmax = d.cmax;
+  if (name) {
+    char buf[96];
+    snprintf(buf, sizeof buf, "conv_lds_%s_%dx%ds%d_%dx%dw%d",
+             d.dtype == WGX_FLOAT32 ? "f32" : (d.dtype == WGX_BFLOAT16 ? "bf16" : "f16"), d.KH, d.KW, d.sH,
+             32 * c.tm, 32 * c.tn, c.w);
+    *name = buf;
+  }
+  if (p.ntiles == 0) return hipSuccess;
+  const unsigned grid = (unsigned)p.ntiles;
+  if (d.dtype == WGX_FLOAT32)
+    return d.sH == 1 ? launch_geo<WGX_FLOAT32, 3, 3, 1>(p, c, grid, s)
+                     : launch_geo<WGX_FLOAT32, 3, 3, 2>(p, c, grid, s);
+  if (d.dtype == WGX_BFLOAT16)
+    return d.sH == 1 ? launch_geo<WGX_BFLOAT16, 3, 3, 1>(p, c, grid, s)
+                     : launch_geo<WGX_BFLOAT16, 3, 3, 2>(p, c, grid, s);
+  return d.sH == 1 ? launch_geo<WGX_FLOAT16, 3, 3, 1>(p, c, grid, s)
+                   : launch_geo<WGX_FLOAT16, 3, 3, 2>(p, c, grid, s);
+}
+
+}  // namespace wgx

@@ -89,6 +89,23 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
 hipError_t noalloc_scratch(int device, void** out);
 hipError_t launch_gemm_f32(const GemmDesc& d, hipStream_t s, std::string* name);
 
+// Dense KxK convolution with each wave's input patch in LDS (conv_lds.hip):
+// groups 1, dilation 1, IC a multiple of 16, 3x3 at stride 1 or 2.
+struct ConvLdsDesc {
+  int dtype;
+  int B, IC, IH, IW, OC, OH, OW, KH, KW, sH, sW, pH, pW;
+  const void* x;
+  const void* w;
+  const void* bias;
+  void* y;
+  int act;  // WGX_ACT_*: applied after the bias, before the clamp
+  int has_clamp;
+  float cmin, cmax;
+};
+bool conv_lds_applies(const ConvLdsDesc& d);
+// cus: compute units of the device (the configuration depends on it)
+hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name);
+
 struct DwDesc {
   int dtype;
   int B, C, IH, IW, OH, OW, KH, KW, sH, sW, pH, pW, dH, dW;

@@ -607,8 +607,10 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
     return r;
   if (bias && (r = c->check(bias, "convolution: bias"))) return r;
   const int dt = in->dtype;
-  if ((dt != WGX_FLOAT32 && dt != WGX_FLOAT16) || weight->dtype != dt || out->dtype != dt)
-    return c->fail(WGX_ERR_INVALID, "convolution: Tensors must have matching float32 or float16 dtype");
+  // bfloat16 is this library's addition (every convolution kernel here is
+  // instantiated for it); the reference takes float32 and float16
+  if ((dt != WGX_FLOAT32 && dt != WGX_FLOAT16 && dt != WGX_BFLOAT16) || weight->dtype != dt || out->dtype != dt)
+    return c->fail(WGX_ERR_INVALID, "convolution: Tensors must have matching float32, float16 or bfloat16 dtype");
   if (bias && bias->dtype != dt) return c->fail(WGX_ERR_INVALID, "convolution: bias dtype must match input dtype");
   if (in->ndim != 4 || weight->ndim != 4 || out->ndim != 4)
     return c->fail(WGX_ERR_INVALID, "convolution: expected 4D tensors for input, weight, and output");
@@ -696,6 +698,42 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
   }
   if (res)
     return c->fail(WGX_ERR_INVALID, "convolution: a residual is supported on depthwise convolutions only");
+  // dense 3x3 convolutions over a multiple of 16 input channels: the
+  // LDS-patch implicit GEMM (no per-element address work)
+  if (!args->transposed && groups == 1 && dH == 1 && dW == 1) {
+    ConvLdsDesc ld{};
+    ld.dtype = dt;
+    ld.B = (int)B;
+    ld.IC = (int)IC;
+    ld.IH = (int)IH;
+    ld.IW = (int)IW;
+    ld.OC = (int)OC;
+    ld.OH = (int)OH;
+    ld.OW = (int)OW;
+    ld.KH = (int)KH;
+    ld.KW = (int)KW;
+    ld.sH = sH;
+    ld.sW = sW;
+    ld.pH = pH;
+    ld.pW = pW;
+    ld.x = in->data;
+    ld.w = weight->data;
+    ld.bias = bias ? bias->data : nullptr;
+    ld.y = out->data;
+    ld.act = act;
+    ld.has_clamp = has_clamp;
+    ld.cmin = cmin;
+    ld.cmax = cmax;
+    if (conv_lds_applies(ld)) {
+      const int cus = device_cu_count(c);
+      e = launch_conv_lds(ld, cus, c->dry(), &name);
+      if (e == hipSuccess)
+        return c->push([ld, cus](hipStream_t s) { return launch_conv_lds(ld, cus, s, nullptr); }, name);
+      if (e != hipErrorInvalidValue) return c->hip_fail(e, "kernel set-up");
+      // a configuration whose LDS does not fit, or a many-tile 16-bit shape
+      // that the GEMM kernels below run faster
+    }
+  }
   const ConvGeom geom{(int)IH, (int)IW, (int)OW, sH, sW, pH, pW, (int)KH, (int)KW, dH, dW};
   // A 1x1 convolution is a plain GEMM with the input plane as its [IC, H*W]
   // operand -- unless it has fewer 64 x 64 output tiles than CUs: then it

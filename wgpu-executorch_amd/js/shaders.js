@@ -7,6 +7,9 @@
  */
 module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
   const isFloatPair = (t) => t.dtype === 'float32' || t.dtype === 'float16';
+  // the GEMM-shaped drivers also take bfloat16 (this backend's addition: the
+  // MFMA kernels run it natively); the reference's message stays the same
+  const isGemmFloat = (t) => isFloatPair(t) || t.dtype === 'bfloat16';
 
   function parseHw(name, v, argName) {
     if (v.length === 1) return [v[0], v[0]];
@@ -32,7 +35,7 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
     code: { f32: 'gemm_f32 (vector FMA, LDS-blocked)', f16: 'gemm_mfma (v_mfma_f32_32x32x16_f16)' },
     recordIn(ctx, [in1, in2, out]) {
       const name = 'aten.mm.default';
-      if (!isFloatPair(in1) || in2.dtype !== in1.dtype || out.dtype !== in1.dtype) {
+      if (!isGemmFloat(in1) || in2.dtype !== in1.dtype || out.dtype !== in1.dtype) {
         throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
       }
       if (in1.shape.length !== 2 || in2.shape.length !== 2 || out.shape.length !== 2) {
@@ -60,7 +63,7 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
       const out = args[args.length - 1];
       const beta = args.length >= 5 && typeof args[3] === 'number' ? args[3] : 1;
       const alpha = args.length >= 6 && typeof args[4] === 'number' ? args[4] : 1;
-      if (!isFloatPair(mat1) || mat2.dtype !== mat1.dtype || out.dtype !== mat1.dtype || bias.dtype !== mat1.dtype) {
+      if (!isGemmFloat(mat1) || mat2.dtype !== mat1.dtype || out.dtype !== mat1.dtype || bias.dtype !== mat1.dtype) {
         throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
       }
       if (mat1.shape.length !== 2 || mat2.shape.length !== 2 || out.shape.length !== 2) {
@@ -82,7 +85,7 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
     code: { f16: 'gemm_mfma NT form (k-contiguous weight rows)' },
     recordIn(ctx, [x, weight, bias, out]) {
       const name = 'aten.linear.default';
-      if (!isFloatPair(x) || weight.dtype !== x.dtype || out.dtype !== x.dtype) {
+      if (!isGemmFloat(x) || weight.dtype !== x.dtype || out.dtype !== x.dtype) {
         throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
       }
       if (x.shape.length !== 2 || weight.shape.length !== 2 || out.shape.length !== 2) {
@@ -101,7 +104,7 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
     code: { f32: 'gemm_f32 batched', f16: 'gemm_mfma batched' },
     recordIn(ctx, [a, b, out]) {
       const name = 'aten.bmm.default';
-      if (!isFloatPair(a) || b.dtype !== a.dtype || out.dtype !== a.dtype) {
+      if (!isGemmFloat(a) || b.dtype !== a.dtype || out.dtype !== a.dtype) {
         throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
       }
       if (a.shape.length !== 3 || b.shape.length !== 3 || out.shape.length !== 3) {
@@ -124,7 +127,7 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
   // after the epilogue (recordProgram's folding of a following add)
   function recordConv(name, ctx, inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding,
     groups, outTensor, clampMin, clampMax, activation, residual) {
-    if (!isFloatPair(inTensor) || weight.dtype !== inTensor.dtype || outTensor.dtype !== inTensor.dtype) {
+    if (!isGemmFloat(inTensor) || weight.dtype !== inTensor.dtype || outTensor.dtype !== inTensor.dtype) {
       throw new Error(`${name}: Tensors must have matching float32 or float16 dtype`);
     }
     if (bias !== undefined && bias.dtype !== inTensor.dtype) {
