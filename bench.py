@@ -9,7 +9,8 @@ step (one captured HIP graph).  Inputs are resident in HBM before timing.
 
 Printed: ONE JSON line on stdout (the contract).  Per-configuration numbers
 for every other configuration (mm 512^3 fp32, the conv pair in fp16 on MFMA,
-depthwise fp16, addmm fp16 NN/NT, bmm fp16) go to stderr and, with --detail
+depthwise fp16, addmm fp16 NN/NT, bmm fp16, the synthetic YOLO-N and the
+reference's yolo26n fp16 programs) go to stderr and, with --detail
 PATH, to a JSON file.  Each is measured at shape (single launch per sample)
 and amortised (a graph of many instances rotating over >= 300 MB of distinct
 buffers, so the 256 MB MALL cannot hold the working set); roofline fractions
@@ -140,8 +141,9 @@ def kernel_probe(W, I, name):
 
 
 def measure_traffic(v):
-    """HBM bytes per step of the headline conv `v` (its GEMM dispatch plus the
-    split-K reduction when there is one) from two rocprofv3 --pmc runs
+    """HBM bytes per step of the headline conv `v` (its convolution or GEMM
+    dispatch, plus the split-K reduction when there is one) from two
+    rocprofv3 --pmc runs
     (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by what the
     counter reads for a plain copy of COPY_BYTES (which moves exactly
     COPY_BYTES in each direction).  The copy's reading is the sum over the
@@ -177,7 +179,7 @@ def measure_traffic(v):
                                      float(row["Counter_Value"])))
             rows.sort()
             conv = [(i, x) for i, n, x in rows
-                    if "k_gemm" in n or "k_sgemm" in n or "k_splitk" in n]
+                    if any(k in n for k in ("k_gemm", "k_sgemm", "k_splitk", "k_conv_lds"))]
             last = max((i for i, _ in conv), default=None)
             copy = [x for i, n, x in rows if "copyBuffer" in n and last is not None and i > last]
             if not conv or not copy:
@@ -336,7 +338,45 @@ def detail_configs(W, I, quick=False, yolo=True):
         log(f"{'5_yolo_n_f16':28s} {y['ops']} ops / {y['commands']} commands      "
             f"frame {y['frame_ms_wall']*1e3:9.1f} us wall (submit+sync), {y['frame_ms_device']*1e3:9.1f} us device  "
             f"{y['conv_GFLOPs_device']:8.1f} conv GFLOP/s")
+    # and the reference's own converted yolo26n (fp16 program and weights)
+    y = yolo26n_frame(quick) if yolo else None
+    if y is not None:
+        out["5_yolo26n_f16"] = y
+        log(f"{'5_yolo26n_f16':28s} {y['ops']} ops / {y['commands']} commands      "
+            f"frame {y['frame_ms_wall']*1e3:9.1f} us wall (submit+sync), {y['frame_ms_device']*1e3:9.1f} us device")
     return out
+
+
+def yolo26n_frame(quick=False):
+    """ms/frame of the reference's yolo26n float16 program (program-fp16.json
+    and weights-fp16.bin as its converter wrote them, 397 operators, input
+    [1,3,640,640]) through recordProgram in Node, measured like yolo_frame."""
+    import shutil
+    import subprocess
+    import tempfile
+
+    node = shutil.which("node")
+    gold = os.path.join(ROOT, "tests", "golden", "yolo26n")
+    if node is None or not os.path.isfile(os.path.join(gold, "program-fp16.json")):
+        log("5_yolo26n_f16: node or the program files are missing, skipped")
+        return None
+    d = tempfile.mkdtemp(prefix="wgx_yolo26n_")
+    try:
+        shutil.copy(os.path.join(gold, "program-fp16.json"), os.path.join(d, "program.json"))
+        os.symlink(os.path.join(gold, "weights-fp16.bin"), os.path.join(d, "weights.bin"))
+        i = np.arange(3 * 640 * 640)
+        ((i % 251) / 250 - 0.5).astype(np.float16).tofile(os.path.join(d, "input.bin"))
+        runner = os.path.join(ROOT, "wgpu-executorch_amd", "js", "run_program.js")
+        reps = 20 if quick else 100
+        r = subprocess.run([node, runner, d, "--device", "0", "--warmup", "5", "--reps", str(reps)],
+                           capture_output=True, text=True, timeout=300)
+        if r.returncode != 0:
+            raise RuntimeError("run_program.js failed: " + r.stderr[-2000:])
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    res["unit"] = "ms/frame"
+    return res
 
 
 def yolo_frame(quick=False):
@@ -512,28 +552,38 @@ def main():
     value = step_flops / (ms_step * 1e-3) / 1e9
 
     # ---- dominant kernel: average launch duration, HIP events recorded on the
-    # context's own stream around one submit of a graph holding REPS launches
-    # of the kernel (the same buffers each time)
-    per_kernel = {}
+    # context's own stream around one submit of a graph, two ways:
+    #  amortised (quoted): AMORT instances over distinct buffers of >= 300 MB
+    #    in all, so the 256 MB MALL cannot hold the working set and every
+    #    launch reads its operands from HBM;
+    #  warm: 20 launches of one instance (operands stay in L2 / MALL).
+    per_kernel, warm = {}, {}
     reps_in_graph = 20
     for v, c in CONV2.items():
         kctx = W.Context(0)
         try:
             build_conv(kctx, I, c, "float32", 40, repeat=reps_in_graph)
-            per_kernel[v] = time_ctx(kctx, 20) / reps_in_graph
+            warm[v] = time_ctx(kctx, 20) / reps_in_graph
         finally:
             kctx.destroy()
+        n = int(300e6 / conv_bytes(c, 4)) + 1
+        _, _, per_kernel[v] = measure(W, lambda ctx, i, c=c: build_conv(ctx, I, c, "float32", 40 + 10 * i), n,
+                                      reps_shape=5, reps_amort=10)
     dom = max(per_kernel, key=per_kernel.get)
     dom_ms = per_kernel[dom]
     achieved = conv_flops(CONV2[dom]) / (dom_ms * 1e-3) / 1e12
+    achieved_warm = conv_flops(CONV2[dom]) / (warm[dom] * 1e-3) / 1e12
     traffic = None if args.no_traffic else measure_traffic(dom)
     roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK["fp32_TFLOPs"],
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK["fp32_TFLOPs"], 4),
                 "traffic": traffic["bytes"] if traffic else None,
                 "kernel": kernels[dom], "workload": f"conv {dom}",
                 "launch_us": round(dom_ms * 1e3, 2),
+                "protocol": "amortised: a graph of instances over >= 300 MB of distinct buffers",
+                "frac_warm": round(achieved_warm / PEAK["fp32_TFLOPs"], 4),
+                "launch_us_warm": round(warm[dom] * 1e3, 2),
                 "launch_covers": ("GEMM dispatch + split-K reduction dispatch"
-                                  if re.search(r"_k\d+$", kernels[dom]) else "GEMM dispatch"),
+                                  if re.search(r"_k\d+$", kernels[dom]) else "one dispatch"),
                 "algorithmic_bytes": conv_bytes(CONV2[dom], 4)}
     if traffic:
         roofline["traffic_detail"] = traffic
