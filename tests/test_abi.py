@@ -126,15 +126,15 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     # 1 (32 x 64 tiles, 64 x 32 for 16-bit data at stride 2, W waves up to
     # the 16-channel chunk count), 64 x 64 one-wave tiles for batched float32,
     # and the GEMM kernels for batched 16-bit data
-    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)) == "conv_lds_f16_3x3s1_32x64w4"
-    assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "conv_lds_f16_3x3s2_64x32w8"
+    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_32x64w4"
+    assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "conv_cl_f16_3x3s2_64x32w8"
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="float32") == "conv_lds_f32_3x3s1_32x64w4"
     assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1), dtype="float32") == "conv_lds_f32_3x3s2_32x64w8"
-    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="bfloat16") == "conv_lds_bf16_3x3s1_32x64w4"
+    assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="bfloat16") == "conv_cl_bf16_3x3s1_32x64w4"
     assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1), dtype="float32") == "conv_lds_f32_3x3s1_64x64w1"
     assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)).startswith("gemm_mfma_f16")
     monkeypatch.setenv("WGX_CONV_LDS", "2x1w2")
-    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_lds_f16_3x3s1_64x32w2"
+    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x32w2"
     monkeypatch.setenv("WGX_CONV_LDS", "off")
     # fewer 64 x 64 tiles than CUs: the wave-split kernel, 64 x 32 tiles with
     # 4 waves (400 of them) or 8 waves (200)

@@ -402,13 +402,16 @@ LDS_CONFIGS = ["2x2w1", "2x2w4", "2x1w2", "1x2w8", "2x1w1"]
 
 
 @pytest.mark.parametrize("cfg", LDS_CONFIGS)
-@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
-def test_lds_patch_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg):
-    """Every configuration of the LDS-patch 3x3 kernel (forced through
-    WGX_CONV_LDS) against the float64 convolution; every second case with a
-    bias, with SiLU or with a clamp in the epilogue."""
+@pytest.mark.parametrize("dtype,form", [("float32", "lds"), ("float16", "cl"), ("bfloat16", "cl"),
+                                        ("float16", "lds"), ("bfloat16", "lds")])
+def test_lds_patch_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, form, cfg):
+    """Every configuration of the LDS-patch 3x3 kernels (forced through
+    WGX_CONV_LDS; 16-bit data in both patch forms, channel-last and
+    channel-major, WGX_CONV_CL) against the float64 convolution; every second
+    case with a bias, with SiLU or with a clamp in the epilogue."""
     W = pkg.wgx
     monkeypatch.setenv("WGX_CONV_LDS", cfg)
+    monkeypatch.setenv("WGX_CONV_CL", "1" if form == "cl" else "0")
     I = pkg.inputs
     for i, (xs, ws, s, p) in enumerate(LDS_CASES):
         x = round_in(I.uniform(900 + i, xs, -1, 1), dtype)
@@ -424,7 +427,7 @@ def test_lds_patch_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg):
                             clamp=(-0.25, 0.5) if mode == 2 else None,
                             activation=W.ACT_SILU if mode == 1 else W.ACT_NONE)
         kernel = gpu_ctx.last_kernel
-        assert kernel.startswith("conv_lds_") and kernel.endswith(
+        assert kernel.startswith(f"conv_{form}_") and kernel.endswith(
             f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}"), kernel
         gpu_ctx.submit()
         gpu_ctx.sync()

@@ -147,11 +147,89 @@ struct Geo {
   }
 };
 
+// Epilogue shared by the convolution kernels: acc[i][j][4g + e] is output
+// channel m0 + i*32 + (lane % 32), region row 4j + g, region column
+// 4*(lane / 32) + e.  With W > 1 waves per block the partial sums of the
+// block's waves meet in LDS and are added in wave order, then bias,
+// activation and clamp, one rounding, 8- or 16-byte stores.
+template <int DT, int TM, int TN>
+__device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM][TN], char* lds, int W, int wave,
+                                              int lane, int m0, int oh0, int ow0, int z, const float (&brow)[TM]) {
+  constexpr int ES = DT == WGX_FLOAT32 ? 4 : 2;
+  constexpr int NG = TM * TN * 4;
+  const int fr = lane & 31, fc = lane >> 5;
+  float* part = reinterpret_cast<float*>(lds);
+  if (W > 1) {
+    __syncthreads();  // every wave is done with its patch
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          reinterpret_cast<float4*>(part)[(wave * NG + (i * TN + j) * 4 + g) * 64 + lane] =
+              make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+    __syncthreads();
+  }
+  const bool vec = (p.OW & 3) == 0;
+  char* yimg = static_cast<char*>(p.y) + (long long)z * p.sy * ES;
+  auto store_group = [&](int q, float4 v) {
+    const int i = q / (TN * 4), j = (q >> 2) % TN, g = q & 3;
+    const int oc = m0 + i * 32 + fr, oh = oh0 + 4 * j + g, ow = ow0 + 4 * fc;
+    if (oc >= p.OC || oh >= p.OH || ow >= p.OW) return;
+    float bias = 0.0f;
+#pragma unroll
+    for (int ii = 0; ii < TM; ++ii)
+      if (ii == i) bias = brow[ii];
+    float vv[4] = {v.x + bias, v.y + bias, v.z + bias, v.w + bias};
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = apply_act(p.act, vv[e]);
+      if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+      h[e] = from_f<DT>(x);
+    }
+    char* dst = yimg + ((long long)oc * p.OH * p.OW + (long long)oh * p.OW + ow) * ES;
+    if (vec && ow + 3 < p.OW) {
+      if constexpr (ES == 4) *reinterpret_cast<uint4*>(dst) = make_uint4(h[0], h[1], h[2], h[3]);
+      else *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (ow + e < p.OW) {
+          if constexpr (ES == 4) reinterpret_cast<uint32_t*>(dst)[e] = h[e];
+          else reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)h[e];
+        }
+    }
+  };
+  if (W == 1) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          store_group((i * TN + j) * 4 + g,
+                      make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]));
+  } else {
+    for (int q = wave; q < NG; q += W) {
+      float4 v = reinterpret_cast<const float4*>(part)[q * 64 + lane];
+      for (int w = 1; w < W; ++w) {
+        const float4 u = reinterpret_cast<const float4*>(part)[(w * NG + q) * 64 + lane];
+        v.x += u.x;
+        v.y += u.y;
+        v.z += u.z;
+        v.w += u.w;
+      }
+      store_group(q, v);
+    }
+  }
+}
+
 template <int DT, int KH, int KW, int S, int TM, int TN>
 __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
   using G = Geo<DT, KH, KW, S, TN>;
   constexpr int ES = G::ES, T = G::T, STEPS = G::STEPS, NBLK = G::NBLK, PF = G::PF;
-  constexpr int NG = TM * TN * 4;  // accumulator groups of 4 per lane
   extern __shared__ uint4 lds_u4[];
   char* lds = reinterpret_cast<char*>(lds_u4);
 
@@ -344,84 +422,217 @@ __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
     asm volatile("" ::: "memory");
   }
 
-  // ------------------------------------------------ epilogue
-  // acc[i][j][4g + e]: output channel m0 + i*32 + fr, region row 4j + g,
-  // region column 4fc + e
-  float* part = reinterpret_cast<float*>(lds);
-  if (W > 1) {
-    __syncthreads();  // every wave is done with its patch
+  conv_epilogue<DT, TM, TN>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+}
+
+// ------------------------------------------------------------ 16-bit form
+// float16 / bfloat16 with a channel-last patch.  Within a chunk of 16 input
+// channels the K order is (tap, channel): step t is tap (kh, kw) = (t / KW,
+// t % KW), lanes 0-31 taking the chunk's channels 0-7 of it and lanes 32-63
+// channels 8-15.  Then
+//   * B: a patch pixel holds its 16 channels in 32 contiguous bytes, so a
+//     lane's B fragment (8 channels of one tap at its output pixel) is ONE
+//     16-byte ds_read at a lane base plus a compile-time tap offset (the
+//     channel-major form above needs one 2-byte ds_read per element);
+//   * A: a lane's 8 channels x T taps are still 8T contiguous elements of its
+//     OIHW weight row (T 16-byte loads per chunk); the fragment of tap t
+//     (elements c*T + t, c = 0..7) is assembled from them in registers.
+// LDS: patch row r starts at r * PW * 32 + (r / S) * 16 bytes; in it column c
+// sits at slot c (S == 1), or (c & 1) * CE + c / 2 (S == 2: the even columns,
+// then the odd ones), 32 bytes a slot.  The 16-byte stagger between the rows
+// that consecutive 8-lane groups read and the column split at stride 2 put
+// the 16 lanes of one LDS cycle on different banks.
+template <int KH, int KW, int S, int TN>
+struct GeoCL {
+  static constexpr int T = KH * KW;
+  static constexpr int RH = 4 * TN, RW = 8;
+  static constexpr int PH = (RH - 1) * S + KH, PW = (RW - 1) * S + KW;
+  static constexpr int PHW = PH * PW;
+  static constexpr int NBLK = (PHW + 63) / 64;  // patch pixels per lane
+  static constexpr int CE = (PW + 1) / 2;      // even columns (S == 2)
+  static constexpr int slot(int c) { return S == 1 ? c : (c & 1) * CE + (c >> 1); }
+  static constexpr int row(int r) { return r * PW * 32 + (r / S) * 16; }
+  static constexpr int LDS_WAVE = row(PH);     // bytes of a wave's patch
+  // tap t relative to the lane's pixel (patch row a*S, column b*S): rows
+  // a*S + kh start row(kh) after row a*S (r / S steps by kh / S), and column
+  // b*S + kw sits slot(kw) after slot b*S
+  static constexpr int toff(int t) { return row(t / KW) + slot(t % KW) * 32; }
+};
+
+template <int DT, int KH, int KW, int S, int TM, int TN>
+__global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p) {
+  using G = GeoCL<KH, KW, S, TN>;
+  constexpr int T = G::T, NBLK = G::NBLK;
+  constexpr int NL = T;  // 16-byte weight loads per row block per chunk (8 channels x T taps)
+  extern __shared__ uint4 lds_u4[];
+  char* lds = reinterpret_cast<char*>(lds_u4);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = p.W;
+  const int fr = lane & 31, fc = lane >> 5;
+  // XCD-aware numbering, output-channel tiles fastest (as in k_conv_lds)
+  const int Gn = gridDim.x;
+  const int rb = (Gn & 7) == 0 ? (blockIdx.x & 7) * (Gn >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  int t0 = rb;
+  const int tm = t0 % p.tiles_m;
+  t0 /= p.tiles_m;
+  const int tw = t0 % p.tiles_w;
+  t0 /= p.tiles_w;
+  const int th = t0 % p.tiles_h;
+  const int z = t0 / p.tiles_h;
+  const int m0 = tm * TM * 32, oh0 = th * G::RH, ow0 = tw * G::RW;
+  const int K = p.IC * T;
+
+  // A: lane offset of its weight row's run (this lane half's 8 channels of
+  // the chunk x T taps); rows past OC read zero
+  uint32_t va[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int oc = m0 + i * 32 + fr;
+    va[i] = oc < p.OC ? (uint32_t)(oc * K + fc * 8 * T) * 2 : OOB;
+  }
+  // patch pixel q = e*64 + lane: its input offset in channel 0 of the chunk
+  // (OOB outside the image) and its LDS slot (-1 past the patch)
+  const int ih0 = oh0 * S - p.pH, iw0 = ow0 * S - p.pW;
+  const int plane = p.IH * p.IW;
+  uint32_t vp[NBLK];
+  int vw[NBLK];
+#pragma unroll
+  for (int e = 0; e < NBLK; ++e) {
+    const int q = e * 64 + lane;
+    const int pr = q / G::PW, pc = q - pr * G::PW;
+    const int ih = ih0 + pr, iw = iw0 + pc;
+    vp[e] = (q < G::PHW && ih >= 0 && ih < p.IH && iw >= 0 && iw < p.IW) ? (uint32_t)(ih * p.IW + iw) * 2 : OOB;
+    vw[e] = q < G::PHW ? G::row(pr) + G::slot(pc) * 32 : -1;
+  }
+  char* wl = lds + wave * G::LDS_WAVE;
+  float brow[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int oc = m0 + i * 32 + fr;
+    brow[i] = (p.bias && oc < p.OC) ? to_f<DT>((uint32_t)reinterpret_cast<const uint16_t*>(p.bias)[oc]) : 0.0f;
+  }
+  // B: the lane's output pixel (row 4j + fr/8, column fr%8 of the region)
+  int vb[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) vb[j] = G::row((4 * j + (fr >> 3)) * S) + (fr & 7) * 32 + fc * 16;
+
+  const char* ximg = static_cast<const char*>(p.x) + (long long)z * p.sx * 2;
+  const char* wbase = static_cast<const char*>(p.w);
+  const uint32_t chunk_x = (uint32_t)(16 * plane * 2), chunk_w = (uint32_t)(16 * T * 2);
+  const uint32_t wbytes = (uint32_t)((long long)p.OC * K * 2);
+  const uint32_t cplane = (uint32_t)(plane * 2);
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // the chunk's patch pixels in registers, channels 2m and 2m+1 in pv[e][m]
+  uint32_t pv[NBLK][8];
+  auto load_patch = [&](int c) {
+    const rsrc_t rx = rsrc(ximg + (long long)c * chunk_x, chunk_x);
+#pragma unroll
+    for (int e = 0; e < NBLK; ++e)
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const uint32_t lo = ld_el<2>(rx, vp[e], 2 * m * cplane), hi = ld_el<2>(rx, vp[e], (2 * m + 1) * cplane);
+        pv[e][m] = lo | (hi << 16);
+      }
+  };
+  auto store_patch = [&]() {
+#pragma unroll
+    for (int e = 0; e < NBLK; ++e)
+      if (vw[e] >= 0) {
+        *reinterpret_cast<uint4*>(wl + vw[e]) = make_uint4(pv[e][0], pv[e][1], pv[e][2], pv[e][3]);
+        *reinterpret_cast<uint4*>(wl + vw[e] + 16) = make_uint4(pv[e][4], pv[e][5], pv[e][6], pv[e][7]);
+      }
+  };
+  // the lane's raw weight run of the next chunk (element c*T + t: channel c,
+  // tap t) and the fragments of the current one
+  uint4 ra[TM][NL];
+  auto load_a = [&](int c) {
+    const rsrc_t rw = rsrc(wbase + (long long)c * chunk_w, wbytes - (uint32_t)c * chunk_w);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int s = 0; s < NL; ++s) ra[i][s] = ld16(rw, va[i], (uint32_t)(s * 16));
+  };
+  uint4 af[T][TM];
+  auto build_a = [&]() {
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          reinterpret_cast<float4*>(part)[(wave * NG + (i * TN + j) * 4 + g) * 64 + lane] =
-              make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-    __syncthreads();
-  }
-  const bool vec = (p.OW & 3) == 0;
-  char* yimg = static_cast<char*>(p.y) + (long long)z * p.sy * ES;
-  auto store_group = [&](int q, float4 v) {
-    const int i = q / (TN * 4), j = (q >> 2) % TN, g = q & 3;
-    const int oc = m0 + i * 32 + fr, oh = oh0 + 4 * j + g, ow = ow0 + 4 * fc;
-    if (oc >= p.OC || oh >= p.OH || ow >= p.OW) return;
-    float bias = 0.0f;
+    for (int i = 0; i < TM; ++i) {
+      uint32_t w[4 * NL];
 #pragma unroll
-    for (int ii = 0; ii < TM; ++ii)
-      if (ii == i) bias = brow[ii];
-    float vv[4] = {v.x + bias, v.y + bias, v.z + bias, v.w + bias};
-    uint32_t h[4];
+      for (int s = 0; s < NL; ++s) {
+        w[4 * s] = ra[i][s].x;
+        w[4 * s + 1] = ra[i][s].y;
+        w[4 * s + 2] = ra[i][s].z;
+        w[4 * s + 3] = ra[i][s].w;
+      }
+      auto h = [&](int q) -> uint32_t { return (q & 1) ? (w[q >> 1] >> 16) : (w[q >> 1] & 0xffffu); };
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float x = apply_act(p.act, vv[e]);
-      if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
-      h[e] = from_f<DT>(x);
-    }
-    char* dst = yimg + ((long long)oc * p.OH * p.OW + (long long)oh * p.OW + ow) * ES;
-    if (vec && ow + 3 < p.OW) {
-      if constexpr (ES == 4) *reinterpret_cast<uint4*>(dst) = make_uint4(h[0], h[1], h[2], h[3]);
-      else *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (ow + e < p.OW) {
-          if constexpr (ES == 4) reinterpret_cast<uint32_t*>(dst)[e] = h[e];
-          else reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)h[e];
-        }
+      for (int t = 0; t < T; ++t)
+        af[t][i] = make_uint4(h(t) | (h(T + t) << 16), h(2 * T + t) | (h(3 * T + t) << 16),
+                              h(4 * T + t) | (h(5 * T + t) << 16), h(6 * T + t) | (h(7 * T + t) << 16));
     }
   };
-  if (W == 1) {
+
+  int c = wave;
+  if (c < p.nchunks) {
+    load_patch(c);
+    load_a(c);
+  }
+  for (; c < p.nchunks; c += W) {
+    const bool more = c + W < p.nchunks;
+    // the patch -> LDS (the previous chunk's reads came first: a wave's LDS
+    // operations run in order), the weights -> fragments, then the next
+    // chunk's loads go out behind this chunk's multiplies
+    store_patch();
+    build_a();
+    asm volatile("" ::: "memory");
+    if (more) {
+      load_patch(c + W);
+      load_a(c + W);
+    }
+    auto read_b = [&](uint4* bf, int t) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const uint4*>(wl + vb[j] + G::toff(t));
+    };
+    uint4 bb[2][TN];
+    read_b(bb[0], 0);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (t + 1 < T) read_b(bb[(t + 1) & 1], t + 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          store_group((i * TN + j) * 4 + g,
-                      make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]));
-  } else {
-    for (int q = wave; q < NG; q += W) {
-      float4 v = reinterpret_cast<const float4*>(part)[q * 64 + lane];
-      for (int w = 1; w < W; ++w) {
-        const float4 u = reinterpret_cast<const float4*>(part)[(w * NG + q) * 64 + lane];
-        v.x += u.x;
-        v.y += u.y;
-        v.z += u.z;
-        v.w += u.w;
-      }
-      store_group(q, v);
+        for (int i = 0; i < TM; ++i) acc[i][j] = mma<DT>(bb[t & 1][j], af[t][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    asm volatile("" ::: "memory");
   }
+
+  conv_epilogue<DT, TM, TN>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
 }
 
 struct Cfg {
   int tm, tn, w;
+  bool cl;  // 16-bit data: the channel-last kernel (else the channel-major one)
 };
 
-template <int DT, int KH, int KW, int S, int TM, int TN>
+template <bool CL, int DT, int KH, int KW, int S, int TM, int TN>
 hipError_t launch_t(const CParams& p, size_t lds, unsigned grid, int w, hipStream_t s) {
-  auto fn = k_conv_lds<DT, KH, KW, S, TM, TN>;
+  void (*fn)(CParams);
+  if constexpr (CL) fn = k_conv_cl<DT, KH, KW, S, TM, TN>;
+  else fn = k_conv_lds<DT, KH, KW, S, TM, TN>;
+  // the channel-last kernel's larger tiles are built for at most 256 threads
+  if (CL && TM * TN >= 4 && w > 4) return hipErrorInvalidValue;
   static bool attr_set = false;
   if (!attr_set && s != name_only()) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -434,27 +645,37 @@ hipError_t launch_t(const CParams& p, size_t lds, unsigned grid, int w, hipStrea
   return hipGetLastError();
 }
 
-template <int DT, int KH, int KW, int S, int TM, int TN>
+template <bool CL, int DT, int KH, int KW, int S, int TM, int TN>
 hipError_t launch_cfg(const CParams& p, const Cfg& c, unsigned grid, hipStream_t s) {
-  using G = Geo<DT, KH, KW, S, TN>;
-  const size_t patch = (size_t)c.w * G::LDS_WAVE;
+  const size_t wave_patch = CL ? (size_t)GeoCL<KH, KW, S, TN>::LDS_WAVE : (size_t)Geo<DT, KH, KW, S, TN>::LDS_WAVE;
+  const size_t patch = (size_t)c.w * wave_patch;
   const size_t part = c.w > 1 ? (size_t)c.w * TM * TN * 4 * 64 * 16 : 0;
   const size_t lds = patch > part ? patch : part;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
-  return launch_t<DT, KH, KW, S, TM, TN>(p, lds, grid, c.w, s);
+  return launch_t<CL, DT, KH, KW, S, TM, TN>(p, lds, grid, c.w, s);
 }
 
 // Instantiated tiles (TM x TN): 32 x 32 up to 64 x 128 (stride 1) and 64 x
 // 64 (stride 2, whose patches are four times larger).
-template <int DT, int KH, int KW, int S>
+template <bool CL, int DT, int KH, int KW, int S>
 hipError_t launch_geo(const CParams& p, const Cfg& c, unsigned grid, hipStream_t s) {
-  if (c.tm == 1 && c.tn == 1) return launch_cfg<DT, KH, KW, S, 1, 1>(p, c, grid, s);
-  if (c.tm == 1 && c.tn == 2) return launch_cfg<DT, KH, KW, S, 1, 2>(p, c, grid, s);
-  if (c.tm == 2 && c.tn == 1) return launch_cfg<DT, KH, KW, S, 2, 1>(p, c, grid, s);
-  if (c.tm == 2 && c.tn == 2) return launch_cfg<DT, KH, KW, S, 2, 2>(p, c, grid, s);
+  if (c.tm == 1 && c.tn == 1) return launch_cfg<CL, DT, KH, KW, S, 1, 1>(p, c, grid, s);
+  if (c.tm == 1 && c.tn == 2) return launch_cfg<CL, DT, KH, KW, S, 1, 2>(p, c, grid, s);
+  if (c.tm == 2 && c.tn == 1) return launch_cfg<CL, DT, KH, KW, S, 2, 1>(p, c, grid, s);
+  if (c.tm == 2 && c.tn == 2) return launch_cfg<CL, DT, KH, KW, S, 2, 2>(p, c, grid, s);
   if constexpr (S == 1)
-    if (c.tm == 2 && c.tn == 4) return launch_cfg<DT, KH, KW, S, 2, 4>(p, c, grid, s);
+    if (c.tm == 2 && c.tn == 4) return launch_cfg<CL, DT, KH, KW, S, 2, 4>(p, c, grid, s);
   return hipErrorInvalidValue;
+}
+
+template <int DT>
+hipError_t launch_dt(const CParams& p, const Cfg& c, int S, unsigned grid, hipStream_t s) {
+  if constexpr (DT == WGX_FLOAT32) {
+    return S == 1 ? launch_geo<false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, DT, 3, 3, 2>(p, c, grid, s);
+  } else {
+    if (c.cl) return S == 1 ? launch_geo<true, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<true, DT, 3, 3, 2>(p, c, grid, s);
+    return S == 1 ? launch_geo<false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, DT, 3, 3, 2>(p, c, grid, s);
+  }
 }
 
 long long tile_count(const ConvLdsDesc& d, const Cfg& c) {
@@ -475,10 +696,11 @@ long long tile_count(const ConvLdsDesc& d, const Cfg& c) {
 Cfg choose(const ConvLdsDesc& d, int cus) {
   const int chunks = d.IC / 16;
   const long long simds = 4LL * cus;
-  Cfg c{2, 2, 1};
+  const bool cl = d.dtype != WGX_FLOAT32 && !(getenv("WGX_CONV_CL") && strcmp(getenv("WGX_CONV_CL"), "0") == 0);
+  Cfg c{2, 2, 1, cl};
   if (tile_count(d, c) < 2 * simds) {
-    if (d.dtype != WGX_FLOAT32 && d.sH == 2) c = Cfg{2, 1, 1};
-    else c = Cfg{1, 2, 1};
+    if (d.dtype != WGX_FLOAT32 && d.sH == 2) c = Cfg{2, 1, 1, cl};
+    else c = Cfg{1, 2, 1, cl};
     const long long tiles = tile_count(d, c);
     int w = 1;
     while (w < 8 && w * 2 <= chunks && tiles * w * 2 <= 4 * simds) w *= 2;
@@ -489,7 +711,7 @@ Cfg choose(const ConvLdsDesc& d, int cus) {
   if (const char* e = getenv("WGX_CONV_LDS")) {
     int tm = 0, tn = 0, ww = 0;
     if (sscanf(e, "%dx%dw%d", &tm, &tn, &ww) == 3 && tm >= 1 && tm <= 2 && tn >= 1 && tn <= 4 && ww >= 1 && ww <= 8)
-      c = Cfg{tm, tn, ww};
+      c = Cfg{tm, tn, ww, cl};
   }
   return c;
 }
@@ -540,21 +762,16 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   p.cmax = d.cmax;
   if (name) {
     char buf[96];
-    snprintf(buf, sizeof buf, "conv_lds_%s_%dx%ds%d_%dx%dw%d",
+    snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d", c.cl ? "cl" : "lds",
              d.dtype == WGX_FLOAT32 ? "f32" : (d.dtype == WGX_BFLOAT16 ? "bf16" : "f16"), d.KH, d.KW, d.sH,
              32 * c.tm, 32 * c.tn, c.w);
     *name = buf;
   }
   if (p.ntiles == 0) return hipSuccess;
   const unsigned grid = (unsigned)p.ntiles;
-  if (d.dtype == WGX_FLOAT32)
-    return d.sH == 1 ? launch_geo<WGX_FLOAT32, 3, 3, 1>(p, c, grid, s)
-                     : launch_geo<WGX_FLOAT32, 3, 3, 2>(p, c, grid, s);
-  if (d.dtype == WGX_BFLOAT16)
-    return d.sH == 1 ? launch_geo<WGX_BFLOAT16, 3, 3, 1>(p, c, grid, s)
-                     : launch_geo<WGX_BFLOAT16, 3, 3, 2>(p, c, grid, s);
-  return d.sH == 1 ? launch_geo<WGX_FLOAT16, 3, 3, 1>(p, c, grid, s)
-                   : launch_geo<WGX_FLOAT16, 3, 3, 2>(p, c, grid, s);
+  if (d.dtype == WGX_FLOAT32) return launch_dt<WGX_FLOAT32>(p, c, d.sH, grid, s);
+  if (d.dtype == WGX_BFLOAT16) return launch_dt<WGX_BFLOAT16>(p, c, d.sH, grid, s);
+  return launch_dt<WGX_FLOAT16>(p, c, d.sH, grid, s);
 }
 
 }  // namespace wgx
