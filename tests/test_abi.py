@@ -92,9 +92,9 @@ def test_mm_validation(hctx, pkg):
     # weight through the [N, K] staging pass
     big = [hctx.tensor("float16", s) for s in ([4096, 768], [768, 3072], [4096, 3072])]
     hctx.mm(*big)
-    assert hctx.last_kernel == "gemm_mfma_f16_256x192w4_kn2nk_big", hctx.last_kernel
+    assert hctx.last_kernel == "gemm_mfma_f16_256x192w8_kn2nk_big", hctx.last_kernel
     hctx.mm(big[0], hctx.tensor("float16", [3072, 768]), big[2], trans_b=True)
-    assert hctx.last_kernel == "gemm_mfma_f16_256x192w4_nk_big", hctx.last_kernel
+    assert hctx.last_kernel == "gemm_mfma_f16_256x192w8_nk_big", hctx.last_kernel
     with pytest.raises(E, match="bias"):
         hctx.mm(*h, bias=hctx.tensor("float16", [7]))
 

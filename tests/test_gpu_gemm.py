@@ -198,7 +198,7 @@ def test_kn_operand_staged_for_large_tile_kernel(gpu_ctx, orc, pkg, tile, monkey
             nt, k_nt = run_mm(gpu_ctx, A, np.ascontiguousarray(B.T), dtype, bias=bias, trans_b=True,
                               alpha=alpha, beta=beta)
             assert k_nn.endswith("_kn2nk_big") and tile[:-1] in k_nn, k_nn
-            assert k_nt.endswith("w4_nk_big"), k_nt
+            assert k_nt.endswith("_nk_big") and not k_nt.endswith("kn2nk_big"), k_nt
             ref, refa = orc.gemm_f64(A, B)
             ref = alpha * ref + beta * bias
             refa = abs(alpha) * refa + abs(beta) * np.abs(bias)

@@ -1196,7 +1196,7 @@ __device__ __forceinline__ int swz64(int r, int c) { return r * 64 + ((c ^ ((r >
 int device_cus();
 
 template <int BM, int BN, int WGM, int WGN, bool BF, int NS, int RB>
-__global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_nk(KParams p) {
+__global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4))) void k_gemm_nk(KParams p) {
   constexpr int NW = WGM * WGN, NT = NW * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
   constexpr int ES = 2, EPC = 8, BK = RB / ES;  // RB: LDS row bytes (64 or 128)
@@ -2394,8 +2394,8 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
     kp.tiles_n = (d.N + b.bn - 1) / b.bn;
     if (name) {
       char buf[96];
-      snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw4_%snk_big", bf ? "bf16" : "f16", b.bm, b.bn,
-               pl.stage_b ? "kn2" : "");
+      snprintf(buf, sizeof buf, "gemm_mfma_%s_%dx%dw%d_%snk_big", bf ? "bf16" : "f16", b.bm, b.bn,
+               b.bm == 256 && b.bn == 192 ? 8 : 4, pl.stage_b ? "kn2" : "");
       *name = buf;
     }
     if (pl.stage_b) {
@@ -2410,7 +2410,7 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
     // 128-byte LDS rows (8 full lines per DMA instruction) and two stages:
     // measured slightly ahead of 64-byte rows with five stages on MI355X
     if (b.bm == 256 && b.bn == 192)
-      return bf ? launch_nk<256, 192, 2, 2, true, 2, 128>(kp, d.batch, s) : launch_nk<256, 192, 2, 2, false, 2, 128>(kp, d.batch, s);
+      return bf ? launch_nk<256, 192, 4, 2, true, 2, 128>(kp, d.batch, s) : launch_nk<256, 192, 4, 2, false, 2, 128>(kp, d.batch, s);
     if (b.bm == 256 && b.bn == 128)
       return bf ? launch_nk<256, 128, 2, 2, true, 3, 128>(kp, d.batch, s) : launch_nk<256, 128, 2, 2, false, 3, 128>(kp, d.batch, s);
     return bf ? launch_nk<192, 256, 2, 2, true, 5, 64>(kp, d.batch, s) : launch_nk<192, 256, 2, 2, false, 5, 64>(kp, d.batch, s);
