@@ -89,20 +89,65 @@ def test_config4_addmm_nn_equals_nt_bitwise(gpu_ctx, pkg):
     assert np.array_equal(nn.view(np.uint32), nt.view(np.uint32))
 
 
-def test_config4_bmm_fp16(gpu_ctx, orc, pkg):
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_config4_bmm_fp16(gpu_ctx, orc, pkg, trans_b):
+    """The config-4 bmm in both layouts of the right operand ([K, N] as given,
+    and its [N, K] transpose with trans_b), every element against fp64; both
+    take the short-K kernel (K = 64, a 16 Mi-element output)."""
     I = pkg.inputs
     A = I.as_f16(I.normal(30, (16, 1024, 64)))
     B = I.as_f16(I.normal(31, (16, 64, 1024)))
-    ta, tb = gpu_ctx.from_numpy(A, "float16"), gpu_ctx.from_numpy(B, "float16")
+    Bop = np.ascontiguousarray(B.transpose(0, 2, 1)) if trans_b else B
+    ta, tb = gpu_ctx.from_numpy(A, "float16"), gpu_ctx.from_numpy(Bop, "float16")
     to = gpu_ctx.tensor("float16", [16, 1024, 1024])
     gpu_ctx.reset()
-    gpu_ctx.bmm(ta, tb, to)
+    gpu_ctx.bmm(ta, tb, to, trans_b=trans_b)
     kernel = gpu_ctx.last_kernel
     gpu_ctx.submit()
     gpu_ctx.sync()
     got = to.get_f32()
     ref, refa = orc.gemm_f64(A, B)
+    assert kernel.endswith(("_nk_sk" if trans_b else "_kn_sk")), kernel
     assert_parity(got, ref, refa, "float16", 64, "bmm " + kernel)
+
+
+SK_SHAPES = [(45, 40, 8), (130, 264, 24), (257, 136, 64), (128, 128, 16), (300, 200, 56), (1, 1000, 40)]
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_short_k_kernel_edges(gpu_ctx, orc, pkg, monkeypatch, dtype, trans_b):
+    """The short-K kernel forced (WGX_SK=1) onto ragged shapes: partial 128 x
+    128 tiles in M and N, K from 8 to 64 (zero-padded to whole k-steps), a
+    batch of 3 and a single row; mm with a column bias, alpha and beta, and
+    bmm; both dtypes and both layouts of B."""
+    monkeypatch.setenv("WGX_SK", "1")
+    I = pkg.inputs
+    for i, (M, N, K) in enumerate(SK_SHAPES):
+        A = round_in(I.uniform(3100 + i, (M, K), -1, 1), dtype)
+        B = round_in(I.uniform(3200 + i, (K, N), -1, 1), dtype)
+        bias = round_in(I.uniform(3300 + i, (N,), -0.5, 0.5), dtype)
+        alpha, beta = (0.5, 2.0) if i % 2 else (1.0, 1.0)
+        Bop = np.ascontiguousarray(B.T) if trans_b else B
+        got, kernel = run_mm(gpu_ctx, A, Bop, dtype, bias=bias, trans_b=trans_b, alpha=alpha, beta=beta)
+        assert kernel.endswith("_sk"), kernel
+        ref, refa = orc.gemm_f64(A, B)
+        ref = alpha * ref + beta * bias
+        refa = abs(alpha) * refa + abs(beta) * np.abs(bias)
+        assert_parity(got, ref, refa, dtype, K, f"sk mm {dtype} {M}x{N}x{K} tb={trans_b} {kernel}")
+        Ab = round_in(I.uniform(3400 + i, (3, M, K), -1, 1), dtype)
+        Bb = round_in(I.uniform(3500 + i, (3, K, N), -1, 1), dtype)
+        Bbop = np.ascontiguousarray(Bb.transpose(0, 2, 1)) if trans_b else Bb
+        ta, tb = gpu_ctx.from_numpy(Ab, dtype), gpu_ctx.from_numpy(Bbop, dtype)
+        to = gpu_ctx.tensor(dtype, [3, M, N])
+        gpu_ctx.reset()
+        gpu_ctx.bmm(ta, tb, to, trans_b=trans_b)
+        kernel = gpu_ctx.last_kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        assert kernel.endswith("_sk"), kernel
+        ref, refa = orc.gemm_f64(Ab, Bb)
+        assert_parity(to.get_f32(), ref, refa, dtype, K, f"sk bmm {dtype} {M}x{N}x{K} tb={trans_b} {kernel}")
 
 
 SHAPES = [(5, 3, 7), (1, 1, 1), (33, 65, 17), (64, 64, 64), (100, 37, 129), (130, 260, 72),

@@ -1472,6 +1472,186 @@ hipError_t launch_nk(const KParams& kp, int batch, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ============================================================ short-K kernel
+// 16-bit GEMMs whose whole K (at most 64) is one LDS slice and whose output is
+// large: aten.bmm [16,1024,64] x [16,64,1024] writes 33.5 MB from 4 MB of
+// operands, so the output path sets the time, not the multiply.  One block of
+// 4 waves owns a 128 x 128 tile: A and B are loaded once into LDS, at most 4
+// k-steps of MFMAs, then the C tile goes through the same LDS and out as
+// whole 256-byte rows (two full 128-byte lines each; partial lines would be
+// merged in L2 or written as masked bursts).  At 35 KB of LDS several blocks
+// share a CU, so one block's stores drain while another loads.
+//   A, and a [N,K] B: LDS rows of 128 bytes (K padded to a multiple of 16
+//     with zeros), 16-byte chunk c of row r at c ^ ((r / 2) % 8), read as
+//     16-byte fragments.
+//   A [K,N] B is read in place: LDS rows k of 288 bytes (128 n and a 32-byte
+//     pad, so the 4 rows one 16-lane group reads start on different banks),
+//     read with the gfx950 transposing read ds_read_b64_tr_b16.  Within each
+//     16-lane group lane L supplies the 4 halves at its address and lane i
+//     receives, as its element e, half i % 4 of lane 4e + i / 4; lane L
+//     pointing at B[k0 + L/4][n0 + 4(L%4)] therefore hands lane i the halves
+//     B[k0 + 0..3][n0 + i]: 4 consecutive k of its column, two reads making
+//     the 8 of an MFMA fragment.
+typedef short v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_tr16(const char* p) {
+  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(const_cast<char*>(p)));
+  return make_uint2(pack2((uint16_t)v.x, (uint16_t)v.y), pack2((uint16_t)v.z, (uint16_t)v.w));
+}
+
+template <bool BF, bool BKN>
+__global__ __launch_bounds__(256) void k_gemm_sk(KParams p) {
+  constexpr int BM = 128, BN = 128, RB = 128, BP = 288, CP = BN * 2 + 16;
+  constexpr int A_BYTES = BM * RB;
+  constexpr int B_BYTES = BKN ? 64 * BP : BN * RB;
+  constexpr int SM = A_BYTES + B_BYTES > BM * CP ? A_BYTES + B_BYTES : BM * CP;
+  __shared__ __attribute__((aligned(16))) char sm[SM];
+  __shared__ __attribute__((aligned(16))) float sbias[128];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves of 64 x 64
+  const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_mn = tiles_m * p.tiles_n;
+  const int z = blockIdx.x / tiles_mn, r = blockIdx.x - z * tiles_mn;
+  const int m0 = (r % tiles_m) * BM, n0 = (r / tiles_m) * BN;
+  const int mrows = min(BM, p.M - m0), nrows = min(BN, p.N - n0);
+  const int K = p.K, KC = K >> 3;  // K <= 64, a multiple of 8: 16-byte chunks per row
+  char* sa = sm;
+  char* sb = sm + A_BYTES;
+
+  // operands -> LDS (rows and chunks past the edges read zero)
+  const rsrc_t ra = make_rsrc(p.A + (long long)z * p.sA + (long long)m0 * p.lda,
+                              (uint32_t)(((long long)(mrows - 1) * p.lda + K) * 2));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+    const uint4 v = ld_b128(ra, row < mrows && ch < KC ? (uint32_t)((row * p.lda + ch * 8) * 2) : OOB);
+    *reinterpret_cast<uint4*>(sa + row * RB + ((ch ^ ((row >> 1) & 7)) << 4)) = v;
+  }
+  if constexpr (BKN) {
+    const rsrc_t rb = make_rsrc(p.B + (long long)z * p.sB + n0, (uint32_t)(((long long)(K - 1) * p.ldb + nrows) * 2));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, row = c >> 4, ch = c & 15;  // row: k
+      const bool ok = row < K && ch * 8 < nrows;
+      const uint4 v = ld_b128(rb, ok ? (uint32_t)((row * p.ldb + ch * 8) * 2) : OOB);
+      *reinterpret_cast<uint4*>(sb + row * BP + ch * 16) = v;
+    }
+  } else {
+    const rsrc_t rb = make_rsrc(p.B + (long long)z * p.sB + (long long)n0 * p.ldb,
+                                (uint32_t)(((long long)(nrows - 1) * p.ldb + K) * 2));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      const uint4 v = ld_b128(rb, row < nrows && ch < KC ? (uint32_t)((row * p.ldb + ch * 8) * 2) : OOB);
+      *reinterpret_cast<uint4*>(sb + row * RB + ((ch ^ ((row >> 1) & 7)) << 4)) = v;
+    }
+  }
+  if (p.bias_mode != BIAS_NONE && tid < 128) {
+    const bool col = p.bias_mode == BIAS_COL;
+    const int lim = col ? p.N : p.M, idx = (col ? n0 : m0) + tid;
+    const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)lim * 2u);
+    sbias[tid] = p.beta * ld_f32<BF>((uint16_t)ld_b16(rbias, idx < lim ? (uint32_t)idx * 2u : OOB));
+  }
+  __syncthreads();
+
+  const int frow = lane & 31, fc = lane >> 5;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  const int KS = (K + 15) >> 4;
+  for (int kk = 0; kk < KS; ++kk) {
+    uint4 a[2], b[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = wm * 64 + i * 32 + frow;
+      a[i] = *reinterpret_cast<const uint4*>(sa + row * RB + (((kk * 2 + fc) ^ ((row >> 1) & 7)) << 4));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if constexpr (BKN) {
+        const int G = lane >> 4, L = lane & 15;
+        const int nb = wn * 64 + j * 32 + (G & 1) * 16, kb = kk * 16 + (G >> 1) * 8;
+        const char* base = sb + (kb + (L >> 2)) * BP + (nb + 4 * (L & 3)) * 2;
+        const uint2 lo = lds_tr16(base), hi = lds_tr16(base + 4 * BP);
+        b[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      } else {
+        const int row = wn * 64 + j * 32 + frow;
+        b[j] = *reinterpret_cast<const uint4*>(sb + row * RB + (((kk * 2 + fc) ^ ((row >> 1) & 7)) << 4));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma<BF>(b[j], a[i], acc[i][j]);
+  }
+  __syncthreads();  // every wave is done with A and B: the memory holds the C tile now
+
+  // acc[i][j]: row wm*64 + i*32 + lane%32, per register group g the columns
+  // wn*64 + j*32 + 8g + 4*(lane/32) + 0..3
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = wm * 64 + i * 32 + frow;
+    const float rowb = p.bias_mode == BIAS_ROW ? sbias[row] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = wn * 64 + j * 32 + 8 * g + 4 * fc;
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = p.alpha * acc[i][j][4 * g + e] + rowb;
+          if (p.bias_mode == BIAS_COL) x += sbias[col + e];
+          x = apply_act(p.act, x);
+          if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+          h[e] = st_bits<BF>(x);
+        }
+        *reinterpret_cast<uint2*>(sm + row * CP + col * 2) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+      }
+  }
+  __syncthreads();
+  // 16 lanes per 256-byte row, 16 rows per pass
+  const rsrc_t rc = make_rsrc(p.C + (long long)z * p.sC + (long long)m0 * p.ldc + n0,
+                              (uint32_t)(((long long)(mrows - 1) * p.ldc + nrows) * 2));
+  const bool cvec = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0) && ((p.sC & 7) == 0);
+#pragma unroll
+  for (int pass = 0; pass < BM / 16; ++pass) {
+    const int row = pass * 16 + (tid >> 4), pc = tid & 15;
+    if (row >= mrows || pc * 8 >= nrows) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(sm + row * CP + pc * 16);
+    const uint32_t off = (uint32_t)((row * p.ldc + pc * 8) * 2);
+    if (cvec && pc * 8 + 8 <= nrows) {
+      if (p.nt_store) {
+        using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+        uint16_t* dst = p.C + (long long)z * p.sC + (long long)(m0 + row) * p.ldc + n0 + pc * 8;
+        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst));
+      } else {
+        st_b128(v, rc, off);
+      }
+    } else {
+      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (pc * 8 + e < nrows) st_b16(u[e >> 1] >> (16 * (e & 1)), rc, off + 2 * e);
+    }
+  }
+}
+
+template <bool BF, bool BKN>
+hipError_t launch_sk(const KParams& kp, int batch, hipStream_t s) {
+  if (is_dry(s)) return hipSuccess;
+  const long long grid = (long long)((kp.M + 127) / 128) * kp.tiles_n * batch;
+  if (grid >= (1LL << 31)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((k_gemm_sk<BF, BKN>), dim3((unsigned)grid), dim3(256), 0, s, kp);
+  return hipGetLastError();
+}
+
 // ============================================================ [K,N] -> [N,K] staging
 // The large-tile kernel reads both operands k-contiguous.  A 16-bit [K, N]
 // operand (aten.mm's own layout) large enough for that kernel is first
@@ -2169,6 +2349,7 @@ struct Plan {
   bool big;        // runs k_gemm_nk with tile bt
   bool stage_b;    // big, on a [K, N] B rewritten as [N, K] first (k_kn_to_nk)
   Tile bt;
+  bool sk;         // runs k_gemm_sk (K <= 64, a large output)
 };
 
 // Large-tile kernel shapes (one block of 4 waves per CU).
@@ -2229,6 +2410,20 @@ Plan make_plan(const GemmDesc& d) {
       }
     }
     pl.stage_b = pl.big && d.bmode == B_KN;
+  }
+  // a short K (one LDS slice) and an output of at least 4 Mi elements: the
+  // time is the output's, which the short-K kernel writes in whole rows.
+  // WGX_SK=0 keeps such GEMMs on the kernels above, WGX_SK=1 takes the
+  // short-K kernel for any output size.
+  {
+    const char* e = getenv("WGX_SK");
+    const bool force = e && e[0] == '1';
+    pl.sk = !pl.f32 && (d.bmode == B_NK || d.bmode == B_KN) && pl.avec && pl.bvec && d.K <= 64 &&
+            (force || (long long)d.batch * d.M * d.N >= (4LL << 20)) && !getenv_is0("WGX_SK");
+  }
+  if (pl.sk) {
+    pl.big = false;
+    pl.stage_b = false;
   }
   return pl;
 }
@@ -2318,7 +2513,7 @@ int gemm_split_plan(const GemmDesc& d, size_t* ws_bytes) {
   *ws_bytes = 0;
   const Plan pl = make_plan(d);
   WsCfg wc;
-  if (!pl.pipelined || pl.big || ws_choice(d, pl, &wc)) return 1;
+  if (!pl.pipelined || pl.big || pl.sk || ws_choice(d, pl, &wc)) return 1;
   const long long ntiles =
       (long long)((d.M + pl.t.bm - 1) / pl.t.bm) * ((d.N + pl.t.bn - 1) / pl.t.bn) * d.batch;
   const int kt = (d.K + 128 / pl.es - 1) / (128 / pl.es);
@@ -2386,6 +2581,19 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
     kp.ws = d.ws;
   }
   kp.nt_store = 0;
+  if (pl.sk && d.splits <= 1) {
+    kp.tiles_n = (d.N + 127) / 128;
+    // outputs of at least 8 MB are written past the caches (bmm config 4:
+    // 18.0 -> 15.7 us measured on MI355X)
+    kp.nt_store = (long long)d.batch * d.M * d.N * es >= (8LL << 20) ? 1 : 0;
+    if (name) {
+      char buf[96];
+      snprintf(buf, sizeof buf, "gemm_mfma_%s_128x128w4_%s_sk", bf ? "bf16" : "f16", d.bmode == B_KN ? "kn" : "nk");
+      *name = buf;
+    }
+    if (d.bmode == B_KN) return bf ? launch_sk<true, true>(kp, d.batch, s) : launch_sk<false, true>(kp, d.batch, s);
+    return bf ? launch_sk<true, false>(kp, d.batch, s) : launch_sk<false, false>(kp, d.batch, s);
+  }
   if (pl.big && d.splits <= 1) {
     // output of at least 8 MB: written past the caches (it does not fit the
     // L2s and the next kernel streams it from HBM either way)
