@@ -399,6 +399,17 @@ LDS_CASES = [
     ((1, 16, 3, 5), (33, 16, 3, 3), 1, 1),
 ]
 LDS_CONFIGS = ["2x2w1", "2x2w4", "2x1w2", "1x2w8", "2x1w1"]
+# float32 chunks are 8 input channels: counts that are not a multiple of 16
+# (the widths that are a multiple of 4 take the row-segment patch loads)
+LDS_CASES_F32 = [
+    ((1, 8, 13, 13), (16, 8, 3, 3), 1, 1),
+    ((2, 24, 10, 9), (40, 24, 3, 3), 2, 1),
+    ((1, 40, 17, 16), (72, 40, 3, 3), 1, 1),
+    ((1, 16, 12, 12), (24, 16, 3, 3), 1, 0),
+    ((2, 8, 9, 16), (32, 8, 3, 3), 2, 1),
+    ((1, 24, 7, 28), (40, 24, 3, 3), 1, 2),
+    ((1, 32, 21, 36), (33, 32, 3, 3), 2, 2),
+]
 
 
 @pytest.mark.parametrize("cfg", LDS_CONFIGS)
@@ -440,3 +451,35 @@ def test_lds_patch_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, form, c
         elif mode == 2:
             ref = np.clip(ref, -0.25, 0.5)
         assert_parity(got, ref, refa, dtype, ws[1] * 9, f"lds {cfg} case {i} {dtype} {xs}x{ws} s{s} p{p} {kernel}")
+
+
+@pytest.mark.parametrize("rv", ["1", "0"])
+@pytest.mark.parametrize("cfg", ["1x2w4", "2x1w2", "1x1w1", "2x2w8"])
+def test_lds_patch_float32_eight_channel_chunks(gpu_ctx, orc, pkg, monkeypatch, cfg, rv):
+    """The float32 LDS-patch kernel on input channel counts that are a
+    multiple of 8 but not of 16 (its chunks are 8 channels), widths with and
+    without the row-segment patch loads (WGX_CONV_RV=0 forces element
+    loads), padding 0 to 2, against the float64 convolution, with a bias and
+    SiLU on every second case."""
+    W, I = pkg.wgx, pkg.inputs
+    monkeypatch.setenv("WGX_CONV_LDS", cfg)
+    monkeypatch.setenv("WGX_CONV_RV", rv)
+    for i, (xs, ws, s, p) in enumerate(LDS_CASES_F32):
+        x = I.uniform(960 + i, xs, -1, 1)
+        w = I.uniform(970 + i, ws, -0.5, 0.5)
+        b = I.uniform(980 + i, (ws[0],), -0.5, 0.5) if i % 2 else None
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), 1)
+        tx, tw = gpu_ctx.from_numpy(x, "float32"), gpu_ctx.from_numpy(w, "float32")
+        tb = gpu_ctx.from_numpy(b, "float32") if b is not None else None
+        ty = gpu_ctx.tensor("float32", list(ref.shape))
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], 1, ty,
+                            activation=W.ACT_SILU if i % 2 else W.ACT_NONE)
+        kernel = gpu_ctx.last_kernel
+        assert kernel.startswith("conv_lds_f32_"), kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        if i % 2:
+            ref = ref / (1.0 + np.exp(-ref))
+            refa = 1.1 * refa
+        assert_parity(ty.get_f32(), ref, refa, "float32", ws[1] * 9, f"lds f32 {cfg} case {i} {xs}x{ws} s{s} {kernel}")

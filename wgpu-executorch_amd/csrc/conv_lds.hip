@@ -1,5 +1,6 @@
 // conv_lds.hip -- dense KxK convolution (groups 1, dilation 1, input channels
-// a multiple of 16) as an implicit GEMM on the gfx950 matrix cores, with each
+// a multiple of 8 for float32, 16 for 16-bit data) as an implicit GEMM on the
+// gfx950 matrix cores, with each
 // wave's input patch in LDS and no per-element address arithmetic.
 //
 // Serves the dense branch of aten.convolution / et_vk.conv_with_clamp
@@ -15,15 +16,16 @@
 // MFMA column block is a 4 x 8 rectangle, so a region's input footprint is a
 // small 2-D patch rather than a row strip).
 //
-// K is walked in chunks of 16 input channels.  Within a chunk the K order is
-// arranged so that both operands need no address work:
-//   * lanes 0-31 take the chunk's channels 0-7 and lanes 32-63 channels 8-15;
-//     each lane half walks its 8 channels x T taps (T = KH*KW) in the
-//     natural (ic, kh, kw) order, 16 bytes at a time;
-//   * A: those 8T k of a weight row are contiguous in OIHW memory, so every
+// K is walked in chunks of 2*CPL input channels (CPL = 8 for 16-bit data, 4
+// for float32).  Within a chunk the K order is arranged so that both operands
+// need no address work:
+//   * lanes 0-31 take the chunk's first CPL channels and lanes 32-63 the
+//     next CPL; each lane half walks its CPL channels x T taps (T = KH*KW) in
+//     the natural (ic, kh, kw) order, 16 bytes at a time;
+//   * A: those CPL*T k of a weight row are contiguous in OIHW memory, so every
 //     A fragment is ONE 16-byte buffer load at a loop-invariant lane offset
 //     plus a compile-time step offset;
-//   * B: the chunk's input patch (16 channels x PH x PW, zero outside the
+//   * B: the chunk's input patch (2*CPL channels x PH x PW, zero outside the
 //     image) sits in the wave's own LDS; the element a lane needs for k =
 //     (channel, kh, kw) of its output pixel is at
 //         pixel_base(lane) + (channel * PH * PW + kh * PW + kw) * ES
@@ -123,19 +125,32 @@ __device__ __forceinline__ uint32_t from_f(float v) {
 // plane (PH x PW, row-major) is padded to whole blocks of 64 elements: patch
 // element (channel, block, lane) sits at (channel * PHWP + block * 64 + lane),
 // so each lane's load targets for every channel differ only by constants.
-template <int DT, int KH, int KW, int S, int TN>
+template <int DT, int KH, int KW, int S, int TN, bool RV = false>
 struct Geo {
   static constexpr int ES = DT == WGX_FLOAT32 ? 4 : 2;
   static constexpr int EPC = 16 / ES;            // k per lane per 16-byte fragment
   static constexpr int T = KH * KW;
-  static constexpr int STEPS = 8 * T / EPC;      // fragments per chunk per lane half
+  // channels per lane half (a chunk is 2*CPL channels): 4 for float32, whose
+  // fragments hold 4 k, so a chunk is 8 channels and a wave of a batch-1
+  // launch gets more of them to pipeline; 8 for 16-bit data
+  static constexpr int CPL = ES == 4 ? 4 : 8;
+  static constexpr int STEPS = CPL * T / EPC;    // fragments per chunk per lane half
   static constexpr int RH = 4 * TN, RW = 8;      // output pixels of the region
   static constexpr int PH = (RH - 1) * S + KH;   // input rows / columns it reads
   static constexpr int PW = (RW - 1) * S + KW;
   static constexpr int PHW = PH * PW;
   static constexpr int NBLK = (PHW + 63) / 64;   // 64-element blocks per channel plane
-  static constexpr int PHWP = NBLK * 64;         // padded plane
-  static constexpr int LDS_WAVE = 16 * PHWP * ES;  // bytes of a wave's patch
+  // Row-segment form (RV: float32, image width a multiple of 4): the patch is
+  // loaded as 16-byte row segments on the image's 4-column grid, so a row
+  // holds PWR >= PW + 3 columns (the region's first column sits 0-3 columns
+  // into it); NRS segments per channel, NPASS passes of 64 lanes.
+  static constexpr int PWR = (PW + 3 + 3) / 4 * 4;
+  static constexpr int NSEG = PWR / 4;
+  static constexpr int NRS = PH * NSEG;
+  static constexpr int NPASS = (NRS + 63) / 64;
+  static constexpr int PHWP = RV ? PH * PWR : NBLK * 64;  // a channel's plane in LDS (elements)
+  static constexpr int ROWP = RV ? PWR : PW;              // its row pitch
+  static constexpr int LDS_WAVE = 2 * CPL * PHWP * ES;  // bytes of a wave's patch
   // A fragments kept in flight ahead of the one being multiplied
   static constexpr int PF = ES == 4 ? STEPS / 3 : STEPS;
   static_assert(STEPS % PF == 0, "the prefetch ring wraps at chunk ends");
@@ -143,7 +158,7 @@ struct Geo {
   // fragment step s (lane half channel = k / T, tap = k % T, k = s*EPC + e)
   static constexpr int boff(int s, int e) {
     const int k = s * EPC + e, ch = k / T, tap = k % T;
-    return (ch * PHWP + (tap / KW) * PW + (tap % KW)) * ES;
+    return (ch * PHWP + (tap / KW) * ROWP + (tap % KW)) * ES;
   }
 };
 
@@ -226,9 +241,10 @@ __device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM
   }
 }
 
-template <int DT, int KH, int KW, int S, int TM, int TN>
+template <int DT, int KH, int KW, int S, int TM, int TN, bool RV>
 __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
-  using G = Geo<DT, KH, KW, S, TN>;
+  using G = Geo<DT, KH, KW, S, TN, RV>;
+  static_assert(!RV || DT == WGX_FLOAT32, "row segments are 4 float32 pixels");
   constexpr int ES = G::ES, T = G::T, STEPS = G::STEPS, NBLK = G::NBLK, PF = G::PF;
   extern __shared__ uint4 lds_u4[];
   char* lds = reinterpret_cast<char*>(lds_u4);
@@ -258,20 +274,36 @@ __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int oc = m0 + i * 32 + fr;
-    va[i] = oc < p.OC ? (uint32_t)(oc * K + fc * 8 * T) * ES : OOB;
+    va[i] = oc < p.OC ? (uint32_t)(oc * K + fc * G::CPL * T) * ES : OOB;
   }
   // patch block e of a channel: this lane's (row, column) of the patch
   // and its input offset in channel 0 of the chunk (OOB outside the image or
   // past the plane)
   const int ih0 = oh0 * S - p.pH, iw0 = ow0 * S - p.pW;
   const int plane = p.IH * p.IW;
-  uint32_t vp[NBLK];
+  constexpr int NVP = RV ? G::NPASS : NBLK;
+  uint32_t vp[NVP];
+  // RV: segment pass e covers row segment q = 64e + lane (row q / NSEG,
+  // columns a0 + 4 (q % NSEG) + 0..3 of the image, a0 = iw0 rounded down to
+  // a multiple of 4: with the width a multiple of 4 a segment is wholly
+  // inside or wholly outside the image); vw: its LDS byte offset, -1 past
+  // the patch
+  const int a0 = iw0 - (((iw0 % 4) + 4) % 4), dl = RV ? iw0 - a0 : 0;
+  int vw[RV ? G::NPASS : 1];
 #pragma unroll
-  for (int e = 0; e < NBLK; ++e) {
+  for (int e = 0; e < NVP; ++e) {
     const int q = e * 64 + lane;
-    const int pr = q / G::PW, pc = q - pr * G::PW;
-    const int ih = ih0 + pr, iw = iw0 + pc;
-    vp[e] = (q < G::PHW && ih >= 0 && ih < p.IH && iw >= 0 && iw < p.IW) ? (uint32_t)(ih * p.IW + iw) * ES : OOB;
+    if constexpr (RV) {
+      const int pr = q / G::NSEG, sg = q - pr * G::NSEG;
+      const int ih = ih0 + pr, col = a0 + 4 * sg;
+      vp[e] = (q < G::NRS && ih >= 0 && ih < p.IH && col >= 0 && col + 4 <= p.IW) ? (uint32_t)(ih * p.IW + col) * ES
+                                                                                    : OOB;
+      vw[e] = q < G::NRS ? q * 16 : -1;
+    } else {
+      const int pr = q / G::PW, pc = q - pr * G::PW;
+      const int ih = ih0 + pr, iw = iw0 + pc;
+      vp[e] = (q < G::PHW && ih >= 0 && ih < p.IH && iw >= 0 && iw < p.IW) ? (uint32_t)(ih * p.IW + iw) * ES : OOB;
+    }
   }
   char* wl = lds + wave * G::LDS_WAVE;
   // B: the lane's output pixel in each 4 x 8 block of the region
@@ -288,11 +320,12 @@ __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
   int vb[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j)
-    vb[j] = (fc * 8 * G::PHWP + ((4 * j + (fr >> 3)) * S) * G::PW + (fr & 7) * S) * ES;
+    vb[j] = (fc * G::CPL * G::PHWP + ((4 * j + (fr >> 3)) * S) * G::ROWP + (fr & 7) * S + dl) * ES;
 
   const char* ximg = static_cast<const char*>(p.x) + (long long)z * p.sx * ES;
   const char* wbase = static_cast<const char*>(p.w);
-  const uint32_t chunk_x = (uint32_t)(16 * plane * ES), chunk_w = (uint32_t)(16 * T * ES);
+  constexpr int CH = 2 * G::CPL;  // channels per chunk
+  const uint32_t chunk_x = (uint32_t)(CH * plane * ES), chunk_w = (uint32_t)(CH * T * ES);
   const uint32_t wbytes = (uint32_t)((long long)p.OC * K * ES);
 
   f32x16 acc[TM][TN];
@@ -303,17 +336,25 @@ __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // the chunk's patch in registers: 16 channels x NBLK blocks (16-bit
+  // the chunk's patch in registers: CH channels x NBLK blocks (16-bit
   // elements two channels to a register)
-  constexpr int NPV = ES == 4 ? 16 * NBLK : 8 * NBLK;
+  constexpr int NPV = RV ? 1 : (ES == 4 ? CH * NBLK : CH / 2 * NBLK);
   uint32_t pv[NPV];
+  uint4 ps[RV ? G::NPASS : 1][RV ? CH : 1];  // RV: the row segments
   const uint32_t cplane = (uint32_t)(plane * ES);
   auto load_patch = [&](int c) {
     const rsrc_t rx = rsrc(ximg + (long long)c * chunk_x, chunk_x);
+    if constexpr (RV) {
+#pragma unroll
+      for (int e = 0; e < G::NPASS; ++e)
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) ps[e][ch] = ld16(rx, vp[e], ch * cplane);
+      return;
+    }
 #pragma unroll
     for (int e = 0; e < NBLK; ++e)
 #pragma unroll
-      for (int ch = 0; ch < 16; ch += (ES == 4 ? 1 : 2)) {
+      for (int ch = 0; ch < CH; ch += (ES == 4 ? 1 : 2)) {
         if constexpr (ES == 4) {
           pv[ch * NBLK + e] = ld_el<4>(rx, vp[e], ch * cplane);
         } else {
@@ -323,10 +364,20 @@ __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
       }
   };
   auto store_patch = [&]() {
+    if constexpr (RV) {
+#pragma unroll
+      for (int e = 0; e < G::NPASS; ++e)
+        if (vw[e] >= 0) {
+#pragma unroll
+          for (int ch = 0; ch < CH; ++ch)
+            *reinterpret_cast<uint4*>(wl + ch * G::PHWP * ES + vw[e]) = ps[e][ch];
+        }
+      return;
+    }
 #pragma unroll
     for (int e = 0; e < NBLK; ++e)
 #pragma unroll
-      for (int ch = 0; ch < 16; ++ch) {
+      for (int ch = 0; ch < CH; ++ch) {
         char* dst = wl + (ch * G::PHWP + e * 64 + lane) * ES;
         if constexpr (ES == 4) *reinterpret_cast<uint32_t*>(dst) = pv[ch * NBLK + e];
         else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(pv[(ch >> 1) * NBLK + e] >> (16 * (ch & 1)));
@@ -624,13 +675,14 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
 struct Cfg {
   int tm, tn, w;
   bool cl;  // 16-bit data: the channel-last kernel (else the channel-major one)
+  bool rv;  // float32: the patch loaded as 16-byte row segments
 };
 
-template <bool CL, int DT, int KH, int KW, int S, int TM, int TN>
+template <bool CL, bool RV, int DT, int KH, int KW, int S, int TM, int TN>
 hipError_t launch_t(const CParams& p, size_t lds, unsigned grid, int w, hipStream_t s) {
   void (*fn)(CParams);
   if constexpr (CL) fn = k_conv_cl<DT, KH, KW, S, TM, TN>;
-  else fn = k_conv_lds<DT, KH, KW, S, TM, TN>;
+  else fn = k_conv_lds<DT, KH, KW, S, TM, TN, RV>;
   // the channel-last kernel's larger tiles are built for at most 256 threads
   if (CL && TM * TN >= 4 && w > 4) return hipErrorInvalidValue;
   static bool attr_set = false;
@@ -645,38 +697,45 @@ hipError_t launch_t(const CParams& p, size_t lds, unsigned grid, int w, hipStrea
   return hipGetLastError();
 }
 
-template <bool CL, int DT, int KH, int KW, int S, int TM, int TN>
+template <bool CL, bool RV, int DT, int KH, int KW, int S, int TM, int TN>
 hipError_t launch_cfg(const CParams& p, const Cfg& c, unsigned grid, hipStream_t s) {
-  const size_t wave_patch = CL ? (size_t)GeoCL<KH, KW, S, TN>::LDS_WAVE : (size_t)Geo<DT, KH, KW, S, TN>::LDS_WAVE;
+  const size_t wave_patch =
+      CL ? (size_t)GeoCL<KH, KW, S, TN>::LDS_WAVE : (size_t)Geo<DT, KH, KW, S, TN, RV>::LDS_WAVE;
   const size_t patch = (size_t)c.w * wave_patch;
   const size_t part = c.w > 1 ? (size_t)c.w * TM * TN * 4 * 64 * 16 : 0;
   const size_t lds = patch > part ? patch : part;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
-  return launch_t<CL, DT, KH, KW, S, TM, TN>(p, lds, grid, c.w, s);
+  return launch_t<CL, RV, DT, KH, KW, S, TM, TN>(p, lds, grid, c.w, s);
 }
 
 // Instantiated tiles (TM x TN): 32 x 32 up to 64 x 128 (stride 1) and 64 x
 // 64 (stride 2, whose patches are four times larger).
-template <bool CL, int DT, int KH, int KW, int S>
+template <bool CL, bool RV, int DT, int KH, int KW, int S>
 hipError_t launch_geo(const CParams& p, const Cfg& c, unsigned grid, hipStream_t s) {
-  if (c.tm == 1 && c.tn == 1) return launch_cfg<CL, DT, KH, KW, S, 1, 1>(p, c, grid, s);
-  if (c.tm == 1 && c.tn == 2) return launch_cfg<CL, DT, KH, KW, S, 1, 2>(p, c, grid, s);
-  if (c.tm == 2 && c.tn == 1) return launch_cfg<CL, DT, KH, KW, S, 2, 1>(p, c, grid, s);
-  if (c.tm == 2 && c.tn == 2) return launch_cfg<CL, DT, KH, KW, S, 2, 2>(p, c, grid, s);
+  if (c.tm == 1 && c.tn == 1) return launch_cfg<CL, RV, DT, KH, KW, S, 1, 1>(p, c, grid, s);
+  if (c.tm == 1 && c.tn == 2) return launch_cfg<CL, RV, DT, KH, KW, S, 1, 2>(p, c, grid, s);
+  if (c.tm == 2 && c.tn == 1) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 1>(p, c, grid, s);
+  if (c.tm == 2 && c.tn == 2) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 2>(p, c, grid, s);
   if constexpr (S == 1)
-    if (c.tm == 2 && c.tn == 4) return launch_cfg<CL, DT, KH, KW, S, 2, 4>(p, c, grid, s);
+    if (c.tm == 2 && c.tn == 4) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 4>(p, c, grid, s);
   return hipErrorInvalidValue;
 }
 
 template <int DT>
 hipError_t launch_dt(const CParams& p, const Cfg& c, int S, unsigned grid, hipStream_t s) {
   if constexpr (DT == WGX_FLOAT32) {
-    return S == 1 ? launch_geo<false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, DT, 3, 3, 2>(p, c, grid, s);
+    if (c.rv)
+      return S == 1 ? launch_geo<false, true, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, true, DT, 3, 3, 2>(p, c, grid, s);
+    return S == 1 ? launch_geo<false, false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, false, DT, 3, 3, 2>(p, c, grid, s);
   } else {
-    if (c.cl) return S == 1 ? launch_geo<true, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<true, DT, 3, 3, 2>(p, c, grid, s);
-    return S == 1 ? launch_geo<false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, DT, 3, 3, 2>(p, c, grid, s);
+    if (c.cl) return S == 1 ? launch_geo<true, false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<true, false, DT, 3, 3, 2>(p, c, grid, s);
+    return S == 1 ? launch_geo<false, false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, false, DT, 3, 3, 2>(p, c, grid, s);
   }
 }
+
+// Input channels per chunk: 8 for float32 (the channel-major kernel's lane
+// halves take 4 each), 16 for 16-bit data (8 per lane half, both kernels).
+int chunk_channels(int dtype) { return dtype == WGX_FLOAT32 ? 8 : 16; }
 
 long long tile_count(const ConvLdsDesc& d, const Cfg& c) {
   return (long long)d.B * ((d.OC + 32 * c.tm - 1) / (32 * c.tm)) * ((d.OH + 4 * c.tn - 1) / (4 * c.tn)) *
@@ -687,14 +746,13 @@ long long tile_count(const ConvLdsDesc& d, const Cfg& c) {
 // 128 (stride 1) and [1,128,80,80] -> 256 (stride 2) at batch 1 and 64:
 //  - few output tiles (under two per SIMD at 64 x 64: batch-1 maps): a 32 x
 //    64 tile (64 x 32 for 16-bit data at stride 2, whose patch is larger) and
-//    W waves per block splitting its 16-channel chunks, W up to the chunk
+//    W waves per block splitting its chunks of input channels, W up to the chunk
 //    count and 8 while the waves stay below four per SIMD;
 //  - many tiles: 64 x 64, one wave per tile, float32 only.  For 16-bit data
 //    the LDS-staged GEMM (gemm_mfma's 128 x 256 conv form) is faster there,
 //    and choose() returns tm = 0: the kernel does not apply.
 // WGX_CONV_LDS=TMxTNwW forces a configuration.
 Cfg choose(const ConvLdsDesc& d, int cus) {
-  const int chunks = d.IC / 16;
   const long long simds = 4LL * cus;
   const bool cl = d.dtype != WGX_FLOAT32 && !(getenv("WGX_CONV_CL") && strcmp(getenv("WGX_CONV_CL"), "0") == 0);
   Cfg c{2, 2, 1, cl};
@@ -703,7 +761,9 @@ Cfg choose(const ConvLdsDesc& d, int cus) {
     else c = Cfg{1, 2, 1, cl};
     const long long tiles = tile_count(d, c);
     int w = 1;
-    while (w < 8 && w * 2 <= chunks && tiles * w * 2 <= 4 * simds) w *= 2;
+    // each wave keeps at least 16 input channels (two float32 chunks, one
+    // 16-bit chunk): [1,64,80,80] float32 16.8 us at 4 waves, 17.3 at 8
+    while (w < 8 && w * 32 <= d.IC && tiles * w * 2 <= 4 * simds) w *= 2;
     c.w = w;
   } else if (d.dtype != WGX_FLOAT32) {
     c.tm = 0;
@@ -721,7 +781,7 @@ Cfg choose(const ConvLdsDesc& d, int cus) {
 bool conv_lds_applies(const ConvLdsDesc& d) {
   if (getenv("WGX_CONV_LDS") && strcmp(getenv("WGX_CONV_LDS"), "off") == 0) return false;
   if (d.dtype != WGX_FLOAT16 && d.dtype != WGX_FLOAT32 && d.dtype != WGX_BFLOAT16) return false;
-  if (d.IC % 16 != 0 || d.IC <= 0 || d.OC <= 0) return false;
+  if (d.IC % chunk_channels(d.dtype) != 0 || d.IC <= 0 || d.OC <= 0) return false;
   const bool geo = (d.KH == 3 && d.KW == 3 && d.sH == d.sW && (d.sH == 1 || d.sH == 2));
   if (!geo) return false;
   const int es = d.dtype == WGX_FLOAT32 ? 4 : 2;
@@ -733,8 +793,13 @@ bool conv_lds_applies(const ConvLdsDesc& d) {
 
 hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name) {
   if (!conv_lds_applies(d)) return hipErrorNotSupported;
-  const Cfg c = choose(d, cus);
+  Cfg c = choose(d, cus);
   if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
+  // float32 images whose width is a multiple of 4 columns (16-byte rows on a
+  // 16-byte base) load the patch as row segments; WGX_CONV_RV=0 keeps the
+  // element loads
+  c.rv = d.dtype == WGX_FLOAT32 && d.IW % 4 == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
+         !(getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0);
   CParams p{};
   p.x = d.x;
   p.w = d.w;
@@ -754,7 +819,7 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   p.tiles_h = (d.OH + 4 * c.tn - 1) / (4 * c.tn);
   p.tiles_w = (d.OW + 7) / 8;
   p.ntiles = d.B * p.tiles_m * p.tiles_h * p.tiles_w;
-  p.nchunks = d.IC / 16;
+  p.nchunks = d.IC / chunk_channels(d.dtype);
   p.W = c.w;
   p.act = d.act;
   p.has_clamp = d.has_clamp;

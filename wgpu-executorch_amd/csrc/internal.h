@@ -90,7 +90,8 @@ hipError_t noalloc_scratch(int device, void** out);
 hipError_t launch_gemm_f32(const GemmDesc& d, hipStream_t s, std::string* name);
 
 // Dense KxK convolution with each wave's input patch in LDS (conv_lds.hip):
-// groups 1, dilation 1, IC a multiple of 16, 3x3 at stride 1 or 2.
+// groups 1, dilation 1, IC a multiple of 8 (float32) or 16 (16-bit data),
+// 3x3 at stride 1 or 2.
 struct ConvLdsDesc {
   int dtype;
   int B, IC, IH, IW, OC, OH, OW, KH, KW, sH, sW, pH, pW;

@@ -698,7 +698,7 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
   }
   if (res)
     return c->fail(WGX_ERR_INVALID, "convolution: a residual is supported on depthwise convolutions only");
-  // dense 3x3 convolutions over a multiple of 16 input channels: the
+  // dense 3x3 convolutions over a multiple of 8 (float32) or 16 input channels: the
   // LDS-patch implicit GEMM (no per-element address work)
   if (!args->transposed && groups == 1 && dH == 1 && dW == 1) {
     ConvLdsDesc ld{};
