@@ -744,9 +744,15 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
   const long long pw_tiles = (OC + 63) / 64 * ((OH * OW + 63) / 64) * B;
   const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0 &&
                          pw_tiles >= device_cu_count(c);
-  // a few taps per output channel (network stems, K = IC*KH*KW <= 32): the
-  // direct small-tap kernel, not a GEMM with a 1-2 step K loop
-  const bool small_taps = !args->transposed && groups == 1 && !pointwise && IC * KH * KW <= 32 && OC <= 64;
+  // a few taps per output channel in a spatial kernel (network stems, K =
+  // IC*KH*KW <= 32, KH*KW > 1): the direct small-tap kernel, not a GEMM with a
+  // 1-2 step K loop ([1,3,640,640]*[16,3,3,3] s2: 14.7 against 28.4 us).  A
+  // 1x1 convolution with few channels stays on the wave-split GEMM:
+  // [1,32,80,80]*[32,32,1,1] 4.3 us there against 23.4 on the small-tap
+  // kernel, [1,16,40,40]*[4,16,1,1] 4.4 against 8.2.
+  const char* st_env = getenv("WGX_SMALL_TAPS");  // "0": never the small-tap kernel
+  const bool small_taps = !args->transposed && groups == 1 && !pointwise && KH * KW > 1 && IC * KH * KW <= 32 &&
+                          OC <= 64 && !(st_env && strcmp(st_env, "0") == 0);
   const bool gemm_ok = !args->transposed && groups == 1 && !small_taps &&
                        (pointwise || conv_ktab_fits((int)(IC * KH * KW), (int)IC, geom));
   if (gemm_ok) {
