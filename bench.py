@@ -411,6 +411,24 @@ def yolo_frame(quick=False):
     return res
 
 
+def gemm_k_sweep(W, I):
+    """Where the large-tile GEMM's time goes: the fp16 addmm NT form (X[4096,K]
+    @ W^T, W^T stored [3072,K], + bias) for K from 64 to 3072, amortised (a
+    graph of instances over >= 300 MB of buffers), one JSON line per K."""
+    M, N = 4096, 3072
+    for K in (64, 192, 384, 768, 1536, 3072):
+        def b(ctx, i, K=K):
+            x = ctx.from_numpy(I.normal(10 * i + 1, (M, K)), "float16")
+            w = ctx.from_numpy(I.normal(10 * i + 2, (N, K), 0, 0.02), "float16")
+            bias = ctx.from_numpy(I.uniform(10 * i + 3, (N,), -0.1, 0.1), "float16")
+            ctx.addmm(bias, x, w, ctx.tensor("float16", [M, N]), trans_b=True)
+            return ctx.last_kernel
+        nbytes = (M * K + N * K + N + M * N) * 2
+        k, s, a = measure(W, b, max(4, int(300e6 // nbytes) + 1), reps_shape=20, reps_amort=5)
+        print(json.dumps({"K": K, "kernel": k, "at_shape_us": round(s * 1e3, 2), "amortised_us": round(a * 1e3, 2),
+                          "TFLOPs_amortised": round(2.0 * M * N * K / (a * 1e-3) / 1e12, 1)}), flush=True)
+
+
 # ---------------------------------------------------------------- vendor libraries
 def vendor_configs():
     """The same shapes through PyTorch-ROCm's own kernels (hipBLASLt for the
@@ -507,6 +525,8 @@ def main():
     ap.add_argument("--no-yolo", action="store_true", help="skip the YOLO-N program (config 5) in the detail")
     ap.add_argument("--kernel-probe", choices=KERNEL_PROBES, default=None,
                     help="record one configuration and submit it a few times (for rocprofv3 --pmc runs)")
+    ap.add_argument("--gemm-k-sweep", action="store_true",
+                    help="time the fp16 addmm NT form at M=4096, N=3072 for K = 64 ... 3072 (amortised) and exit")
     ap.add_argument("--vendor-probe", action="store_true",
                     help=argparse.SUPPRESS)  # the child run that times the vendor kernels
     ap.add_argument("--traffic-probe", choices=list(CONV2), default=None,
@@ -531,6 +551,9 @@ def main():
         return
     if args.kernel_probe:
         kernel_probe(W, I, args.kernel_probe)
+        return
+    if args.gemm_k_sweep:
+        gemm_k_sweep(W, I)
         return
 
     # ---- headline: config 2 (2a + 2b), float32, one submit per step
