@@ -1500,154 +1500,217 @@ __device__ __forceinline__ uint2 lds_tr16(const char* p) {
 }
 
 template <bool BF, bool BKN>
-__global__ __launch_bounds__(256) void k_gemm_sk(KParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_sk(KParams p) {
   constexpr int BM = 128, BN = 128, RB = 128, BP = 288, CP = BN * 2 + 16;
   constexpr int A_BYTES = BM * RB;
   constexpr int B_BYTES = BKN ? 64 * BP : BN * RB;
-  constexpr int SM = A_BYTES + B_BYTES > BM * CP ? A_BYTES + B_BYTES : BM * CP;
-  __shared__ __attribute__((aligned(16))) char sm[SM];
-  __shared__ __attribute__((aligned(16))) float sbias[128];
+  __shared__ __attribute__((aligned(16))) char sab[A_BYTES + B_BYTES];
+  __shared__ __attribute__((aligned(16))) char sc[BM * CP];
+  // the bias of the tile's rows and of its columns (the one not in use holds
+  // zeros), so the epilogue adds both without a branch
+  __shared__ __attribute__((aligned(16))) float srow[128], scol[128];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves of 64 x 64
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_mn = tiles_m * p.tiles_n;
-  const int z = blockIdx.x / tiles_mn, r = blockIdx.x - z * tiles_mn;
-  const int m0 = (r % tiles_m) * BM, n0 = (r / tiles_m) * BN;
-  const int mrows = min(BM, p.M - m0), nrows = min(BN, p.N - n0);
+  const int ntiles = tiles_mn * p.batch;
   const int K = p.K, KC = K >> 3;  // K <= 64, a multiple of 8: 16-byte chunks per row
-  char* sa = sm;
-  char* sb = sm + A_BYTES;
+  const int KS = (K + 15) >> 4;
+  char* sa = sab;
+  char* sb = sab + A_BYTES;
+  const int frow = lane & 31, fc = lane >> 5;
 
-  // operands -> LDS (rows and chunks past the edges read zero)
-  const rsrc_t ra = make_rsrc(p.A + (long long)z * p.sA + (long long)m0 * p.lda,
-                              (uint32_t)(((long long)(mrows - 1) * p.lda + K) * 2));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-    const uint4 v = ld_b128(ra, row < mrows && ch < KC ? (uint32_t)((row * p.lda + ch * 8) * 2) : OOB);
-    *reinterpret_cast<uint4*>(sa + row * RB + ((ch ^ ((row >> 1) & 7)) << 4)) = v;
-  }
-  if constexpr (BKN) {
-    const rsrc_t rb = make_rsrc(p.B + (long long)z * p.sB + n0, (uint32_t)(((long long)(K - 1) * p.ldb + nrows) * 2));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i, row = c >> 4, ch = c & 15;  // row: k
-      const bool ok = row < K && ch * 8 < nrows;
-      const uint4 v = ld_b128(rb, ok ? (uint32_t)((row * p.ldb + ch * 8) * 2) : OOB);
-      *reinterpret_cast<uint4*>(sb + row * BP + ch * 16) = v;
-    }
-  } else {
-    const rsrc_t rb = make_rsrc(p.B + (long long)z * p.sB + (long long)n0 * p.ldb,
-                                (uint32_t)(((long long)(nrows - 1) * p.ldb + K) * 2));
+  struct TileAt {
+    int z, m0, n0, mrows, nrows;
+  };
+  auto tile_at = [&](int t) {
+    TileAt ti;
+    ti.z = t / tiles_mn;
+    const int r = t - ti.z * tiles_mn;
+    ti.m0 = (r % tiles_m) * BM;
+    ti.n0 = (r / tiles_m) * BN;
+    ti.mrows = min(BM, p.M - ti.m0);
+    ti.nrows = min(BN, p.N - ti.n0);
+    return ti;
+  };
+
+  // a tile's operands in registers: 4 16-byte chunks of A and 4 of B per
+  // thread and one bias element; a tile index past the end reads zeros
+  uint4 ra[4], rb[4];
+  uint32_t rbias;
+  auto load_regs = [&](int t) {
+    const bool ok = t < ntiles;
+    const TileAt ti = tile_at(ok ? t : 0);
+    const rsrc_t rsa = make_rsrc(p.A + (long long)ti.z * p.sA + (long long)ti.m0 * p.lda,
+                                 (uint32_t)(((long long)(ti.mrows - 1) * p.lda + K) * 2));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      const uint4 v = ld_b128(rb, row < nrows && ch < KC ? (uint32_t)((row * p.ldb + ch * 8) * 2) : OOB);
-      *reinterpret_cast<uint4*>(sb + row * RB + ((ch ^ ((row >> 1) & 7)) << 4)) = v;
+      ra[i] = ld_b128(rsa, ok && row < ti.mrows && ch < KC ? (uint32_t)((row * p.lda + ch * 8) * 2) : OOB);
     }
-  }
-  if (p.bias_mode != BIAS_NONE && tid < 128) {
+    if constexpr (BKN) {
+      const rsrc_t rsb = make_rsrc(p.B + (long long)ti.z * p.sB + ti.n0,
+                                   (uint32_t)(((long long)(K - 1) * p.ldb + ti.nrows) * 2));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i, row = c >> 4, ch = c & 15;  // row: k
+        rb[i] = ld_b128(rsb, ok && row < K && ch * 8 < ti.nrows ? (uint32_t)((row * p.ldb + ch * 8) * 2) : OOB);
+      }
+    } else {
+      const rsrc_t rsb = make_rsrc(p.B + (long long)ti.z * p.sB + (long long)ti.n0 * p.ldb,
+                                   (uint32_t)(((long long)(ti.nrows - 1) * p.ldb + K) * 2));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+        rb[i] = ld_b128(rsb, ok && row < ti.nrows && ch < KC ? (uint32_t)((row * p.ldb + ch * 8) * 2) : OOB);
+      }
+    }
     const bool col = p.bias_mode == BIAS_COL;
-    const int lim = col ? p.N : p.M, idx = (col ? n0 : m0) + tid;
-    const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)lim * 2u);
-    sbias[tid] = p.beta * ld_f32<BF>((uint16_t)ld_b16(rbias, idx < lim ? (uint32_t)idx * 2u : OOB));
-  }
-  __syncthreads();
-
-  const int frow = lane & 31, fc = lane >> 5;
-  f32x16 acc[2][2];
+    const int lim = col ? p.N : p.M, idx = (col ? ti.n0 : ti.m0) + (tid & 127);
+    const rsrc_t rsbias = make_rsrc(p.bias, p.bias_mode != BIAS_NONE ? (uint32_t)lim * 2u : 0u);
+    rbias = ld_b16(rsbias, ok && idx < lim ? (uint32_t)idx * 2u : OOB);
+  };
+  // registers -> LDS (zeros stand for rows and chunks past the edges)
+  auto store_lds = [&]() {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      *reinterpret_cast<uint4*>(sa + row * RB + ((ch ^ ((row >> 1) & 7)) << 4)) = ra[i];
+    }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-  const int KS = (K + 15) >> 4;
-  for (int kk = 0; kk < KS; ++kk) {
-    uint4 a[2], b[2];
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (BKN) {
+        const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+        *reinterpret_cast<uint4*>(sb + row * BP + ch * 16) = rb[i];
+      } else {
+        const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+        *reinterpret_cast<uint4*>(sb + row * RB + ((ch ^ ((row >> 1) & 7)) << 4)) = rb[i];
+      }
+    }
+    if (tid < 128) {
+      const float v = p.beta * ld_f32<BF>((uint16_t)rbias);
+      srow[tid] = p.bias_mode == BIAS_ROW ? v : 0.0f;
+      scol[tid] = p.bias_mode == BIAS_COL ? v : 0.0f;
+    }
+  };
+  // acc[i][j]: row wm*64 + i*32 + lane%32, per register group g the columns
+  // wn*64 + j*32 + 8g + 4*(lane/32) + 0..3 -> the C stage
+  auto epilogue = [&]<bool PLAIN>(const f32x16 (&acc)[2][2]) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int row = wm * 64 + i * 32 + frow;
-      a[i] = *reinterpret_cast<const uint4*>(sa + row * RB + (((kk * 2 + fc) ^ ((row >> 1) & 7)) << 4));
-    }
+      const float rowb = srow[row];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if constexpr (BKN) {
-        const int G = lane >> 4, L = lane & 15;
-        const int nb = wn * 64 + j * 32 + (G & 1) * 16, kb = kk * 16 + (G >> 1) * 8;
-        const char* base = sb + (kb + (L >> 2)) * BP + (nb + 4 * (L & 3)) * 2;
-        const uint2 lo = lds_tr16(base), hi = lds_tr16(base + 4 * BP);
-        b[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-      } else {
-        const int row = wn * 64 + j * 32 + frow;
-        b[j] = *reinterpret_cast<const uint4*>(sb + row * RB + (((kk * 2 + fc) ^ ((row >> 1) & 7)) << 4));
-      }
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = wn * 64 + j * 32 + 8 * g + 4 * fc;
+          const float4 cb = *reinterpret_cast<const float4*>(scol + col);
+          const float colb[4] = {cb.x, cb.y, cb.z, cb.w};
+          uint32_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float x = p.alpha * acc[i][j][4 * g + e] + rowb + colb[e];
+            if constexpr (!PLAIN) {
+              x = apply_act(p.act, x);
+              if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+            }
+            h[e] = st_bits<BF>(x);
+          }
+          *reinterpret_cast<uint2*>(sc + row * CP + col * 2) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+        }
     }
+  };
+  // the C stage -> global memory, 16 lanes per 256-byte row, 16 rows per
+  // pass; every store is issued (a piece past the tile's edge at an
+  // out-of-range offset, which the buffer range check drops), so the count of
+  // stores in flight is the same on every path.  aux 2: non-temporal.
+  auto store_c = [&]<int AUX>(const TileAt& ti) {
+    const rsrc_t rc = make_rsrc(p.C + (long long)ti.z * p.sC + (long long)ti.m0 * p.ldc + ti.n0,
+                                (uint32_t)(((long long)(ti.mrows - 1) * p.ldc + ti.nrows) * 2));
+    using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int pass = 0; pass < BM / 16; ++pass) {
+      const int row = pass * 16 + (tid >> 4), pc = tid & 15;
+      const uint4 v = *reinterpret_cast<const uint4*>(sc + row * CP + pc * 16);
+      const bool in = row < ti.mrows && pc * 8 < ti.nrows;
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, rc,
+                                             in ? (int)((row * p.ldc + pc * 8) * 2) : (int)OOB, 0, AUX);
+    }
+  };
+  const bool plain = p.act == WGX_ACT_NONE && !p.has_clamp;
+
+  int t = blockIdx.x;
+  load_regs(t);
+  store_lds();
+  for (; t < ntiles; t += gridDim.x) {
+    const TileAt ti = tile_at(t);
+    // this tile's operands are in LDS; every wave has read the previous C stage
+    __syncthreads();
+    // the next tile's operands are in flight during this tile's multiplies
+    load_regs(t + gridDim.x);
+
+    f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = mfma<BF>(b[j], a[i], acc[i][j]);
-  }
-  __syncthreads();  // every wave is done with A and B: the memory holds the C tile now
-
-  // acc[i][j]: row wm*64 + i*32 + lane%32, per register group g the columns
-  // wn*64 + j*32 + 8g + 4*(lane/32) + 0..3
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = wm * 64 + i * 32 + frow;
-    const float rowb = p.bias_mode == BIAS_ROW ? sbias[row] : 0.0f;
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int kk = 0; kk < KS; ++kk) {
+      uint4 a[2], b[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int i = 0; i < 2; ++i) {
+        const int row = wm * 64 + i * 32 + frow;
+        a[i] = *reinterpret_cast<const uint4*>(sa + row * RB + (((kk * 2 + fc) ^ ((row >> 1) & 7)) << 4));
+      }
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col = wn * 64 + j * 32 + 8 * g + 4 * fc;
-        uint32_t h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float x = p.alpha * acc[i][j][4 * g + e] + rowb;
-          if (p.bias_mode == BIAS_COL) x += sbias[col + e];
-          x = apply_act(p.act, x);
-          if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
-          h[e] = st_bits<BF>(x);
+      for (int j = 0; j < 2; ++j) {
+        if constexpr (BKN) {
+          const int G = lane >> 4, L = lane & 15;
+          const int nb = wn * 64 + j * 32 + (G & 1) * 16, kb = kk * 16 + (G >> 1) * 8;
+          const char* base = sb + (kb + (L >> 2)) * BP + (nb + 4 * (L & 3)) * 2;
+          const uint2 lo = lds_tr16(base), hi = lds_tr16(base + 4 * BP);
+          b[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        } else {
+          const int row = wn * 64 + j * 32 + frow;
+          b[j] = *reinterpret_cast<const uint4*>(sb + row * RB + (((kk * 2 + fc) ^ ((row >> 1) & 7)) << 4));
         }
-        *reinterpret_cast<uint2*>(sm + row * CP + col * 2) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
       }
-  }
-  __syncthreads();
-  // 16 lanes per 256-byte row, 16 rows per pass
-  const rsrc_t rc = make_rsrc(p.C + (long long)z * p.sC + (long long)m0 * p.ldc + n0,
-                              (uint32_t)(((long long)(mrows - 1) * p.ldc + nrows) * 2));
-  const bool cvec = ((p.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0) && ((p.sC & 7) == 0);
 #pragma unroll
-  for (int pass = 0; pass < BM / 16; ++pass) {
-    const int row = pass * 16 + (tid >> 4), pc = tid & 15;
-    if (row >= mrows || pc * 8 >= nrows) continue;
-    const uint4 v = *reinterpret_cast<const uint4*>(sm + row * CP + pc * 16);
-    const uint32_t off = (uint32_t)((row * p.ldc + pc * 8) * 2);
-    if (cvec && pc * 8 + 8 <= nrows) {
-      if (p.nt_store) {
-        using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
-        uint16_t* dst = p.C + (long long)z * p.sC + (long long)(m0 + row) * p.ldc + n0 + pc * 8;
-        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst));
-      } else {
-        st_b128(v, rc, off);
-      }
-    } else {
-      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (pc * 8 + e < nrows) st_b16(u[e >> 1] >> (16 * (e & 1)), rc, off + 2 * e);
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma<BF>(b[j], a[i], acc[i][j]);
     }
+    if (plain)
+      epilogue.template operator()<true>(acc);
+    else
+      epilogue.template operator()<false>(acc);
+    // the C stage is whole; every wave is done with the operands and the bias
+    __syncthreads();
+    // the next tile's operands -> LDS (waits for their loads, issued before
+    // this tile's multiplies), then this tile's stores, which drain during
+    // the next tile's multiplies
+    store_lds();
+    if (p.nt_store)
+      store_c.template operator()<2>(ti);
+    else
+      store_c.template operator()<0>(ti);
   }
 }
 
 template <bool BF, bool BKN>
 hipError_t launch_sk(const KParams& kp, int batch, hipStream_t s) {
   if (is_dry(s)) return hipSuccess;
-  const long long grid = (long long)((kp.M + 127) / 128) * kp.tiles_n * batch;
-  if (grid >= (1LL << 31)) return hipErrorInvalidValue;
+  const long long ntiles = (long long)((kp.M + 127) / 128) * kp.tiles_n * batch;
+  if (ntiles >= (1LL << 31)) return hipErrorInvalidValue;
+  // persistent: two blocks per CU (about 70 KB of LDS each), block b walking
+  // tiles b, b + grid, ...
+  long long grid = 2LL * device_cus();
+  if (const char* e = getenv("WGX_SK_BLOCKS")) grid = atoll(e) > 0 ? atoll(e) : grid;
+  if (grid > ntiles) grid = ntiles;
   hipLaunchKernelGGL((k_gemm_sk<BF, BKN>), dim3((unsigned)grid), dim3(256), 0, s, kp);
   return hipGetLastError();
 }
@@ -2418,7 +2481,8 @@ Plan make_plan(const GemmDesc& d) {
   {
     const char* e = getenv("WGX_SK");
     const bool force = e && e[0] == '1';
-    pl.sk = !pl.f32 && (d.bmode == B_NK || d.bmode == B_KN) && pl.avec && pl.bvec && d.K <= 64 &&
+    const bool cvec = (d.N % 8 == 0) && (d.ldc % 8 == 0) && (d.sC % 8 == 0) && aligned16(d.C);
+    pl.sk = !pl.f32 && (d.bmode == B_NK || d.bmode == B_KN) && pl.avec && pl.bvec && cvec && d.K <= 64 &&
             (force || (long long)d.batch * d.M * d.N >= (4LL << 20)) && !getenv_is0("WGX_SK");
   }
   if (pl.sk) {
@@ -2583,6 +2647,7 @@ hipError_t launch_gemm_mfma(const GemmDesc& d, hipStream_t s, std::string* name)
   kp.nt_store = 0;
   if (pl.sk && d.splits <= 1) {
     kp.tiles_n = (d.N + 127) / 128;
+    kp.batch = d.batch;
     // outputs of at least 8 MB are written past the caches (bmm config 4:
     // 18.0 -> 15.7 us measured on MI355X)
     kp.nt_store = (long long)d.batch * d.M * d.N * es >= (8LL << 20) ? 1 : 0;
