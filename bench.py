@@ -103,15 +103,16 @@ def traffic_probe(W, I, v):
 
 # One configuration, recorded once and submitted PROBE_REPS times without a
 # graph (one dispatch per launch): the child run that rocprofv3 --pmc counts.
-KERNEL_PROBES = ("conv2a_f32", "conv2b_f32", "conv2a_f16", "addmm_nt", "addmm_nn", "bmm",
-                 "dw3a", "dw3b", "dw3a_b256", "dw3b_b256")
+KERNEL_PROBES = ("conv2a_f32", "conv2b_f32", "conv2a_f16", "conv2a_f16_b64", "conv2b_f16_b64", "addmm_nt",
+                 "addmm_nn", "bmm", "dw3a", "dw3b", "dw3a_b256", "dw3b_b256")
 
 
 def kernel_probe(W, I, name):
     ctx = W.Context(0)
     try:
         if name.startswith("conv"):
-            build_conv(ctx, I, CONV2[name[4:6]], "float32" if name.endswith("f32") else "float16", 40)
+            build_conv(ctx, I, CONV2[name[4:6]], "float32" if name.endswith("f32") else "float16", 40,
+                       batch=64 if name.endswith("_b64") else 1)
         elif name.startswith("addmm"):
             M, K, N = 4096, 768, 3072
             nt = name.endswith("nt")

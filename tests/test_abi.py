@@ -125,14 +125,20 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     # dense 3x3 over a multiple of 16 channels: the LDS-patch kernel at batch
     # 1 (32 x 64 tiles, 64 x 32 for 16-bit data at stride 2, W waves up to
     # the 16-channel chunk count), 64 x 64 one-wave tiles for batched float32,
-    # and the GEMM kernels for batched 16-bit data
+    # for batched 16-bit data at stride 1 the 64 x 128 channel-last tile while
+    # it gives every SIMD a wave, else the GEMM kernels
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_32x64w4"
     assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "conv_cl_f16_3x3s2_64x32w8"
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="float32") == "conv_lds_f32_3x3s1_32x64w4"
     assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1), dtype="float32") == "conv_lds_f32_3x3s2_32x64w8"
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="bfloat16") == "conv_cl_bf16_3x3s1_32x64w4"
     assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1), dtype="float32") == "conv_lds_f32_3x3s1_64x64w1"
-    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)).startswith("gemm_mfma_f16")
+    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x128w1"
+    assert conv([64, 64, 80, 80], [128, 64, 3, 3], [64, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x128w1"
+    assert conv([8, 32, 160, 160], [64, 32, 3, 3], [8, 64, 160, 160], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x128w1"
+    assert conv([16, 128, 40, 40], [256, 128, 3, 3], [16, 256, 40, 40], pad=(1, 1)).startswith("gemm_mfma_f16")
+    assert conv([64, 128, 80, 80], [256, 128, 3, 3], [64, 256, 40, 40], (2, 2), (1, 1)).startswith("gemm_mfma_f16")
+    assert conv([4, 64, 80, 80], [128, 64, 3, 3], [4, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_32x64w2"
     monkeypatch.setenv("WGX_CONV_LDS", "2x1w2")
     assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x32w2"
     monkeypatch.setenv("WGX_CONV_LDS", "off")

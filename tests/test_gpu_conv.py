@@ -453,6 +453,78 @@ def test_lds_patch_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, form, c
         assert_parity(got, ref, refa, dtype, ws[1] * 9, f"lds {cfg} case {i} {dtype} {xs}x{ws} s{s} p{p} {kernel}")
 
 
+# 16-bit images whose width is a multiple of 8 columns (the channel-last
+# kernel's row-segment patch loads): every patch offset within a segment
+# (padding 0, 1, 2 at both strides), maps narrower than a segment row,
+# ragged output channels and batch 2
+CL_SEG_CASES = [
+    ((1, 16, 16, 16), (24, 16, 3, 3), 1, 1),
+    ((2, 32, 15, 24), (40, 32, 3, 3), 1, 1),
+    ((1, 64, 20, 40), (64, 64, 3, 3), 1, 0),
+    ((1, 32, 10, 16), (100, 32, 3, 3), 2, 1),
+    ((2, 48, 33, 32), (72, 48, 3, 3), 2, 1),
+    ((1, 16, 9, 8), (16, 16, 3, 3), 1, 2),
+    ((1, 32, 12, 24), (8, 32, 3, 3), 2, 2),
+    ((1, 16, 3, 8), (33, 16, 3, 3), 1, 1),
+    ((1, 32, 17, 40), (64, 32, 3, 3), 2, 0),
+]
+
+
+@pytest.mark.parametrize("rv", ["1", "0"])
+@pytest.mark.parametrize("cfg", ["2x4w1", "2x2w1", "2x2w4", "1x2w8", "1x1w1"])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_channel_last_row_segments(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg, rv):
+    """The channel-last 16-bit kernel with its patch loaded as 16-byte row
+    segments turned channel-last in registers (WGX_CONV_RV=1) and as element
+    loads (WGX_CONV_RV=0), forced into each configuration, against the
+    float64 convolution; a bias and SiLU on every second case.  The 64 x 128
+    tile (2x4) is built for stride 1 only."""
+    W, I = pkg.wgx, pkg.inputs
+    monkeypatch.setenv("WGX_CONV_LDS", cfg)
+    monkeypatch.setenv("WGX_CONV_CL", "1")
+    monkeypatch.setenv("WGX_CONV_RV", rv)
+    for i, (xs, ws, s, p) in enumerate(CL_SEG_CASES):
+        if cfg == "2x4w1" and s != 1:
+            continue
+        x = round_in(I.uniform(1900 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(1910 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(1920 + i, (ws[0],), -0.5, 0.5), dtype) if i % 2 else None
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), 1)
+        tx, tw = gpu_ctx.from_numpy(x, dtype), gpu_ctx.from_numpy(w, dtype)
+        tb = gpu_ctx.from_numpy(b, dtype) if b is not None else None
+        ty = gpu_ctx.tensor(dtype, list(ref.shape))
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], 1, ty,
+                            activation=W.ACT_SILU if i % 2 else W.ACT_NONE)
+        kernel = gpu_ctx.last_kernel
+        assert kernel.startswith("conv_cl_") and kernel.endswith(
+            f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}"), kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        if i % 2:
+            ref = ref / (1.0 + np.exp(-ref))
+            refa = 1.1 * refa
+        assert_parity(ty.get_f32(), ref, refa, dtype, ws[1] * 9,
+                      f"cl seg rv={rv} {cfg} case {i} {dtype} {xs}x{ws} s{s} p{p} {kernel}")
+
+
+def test_batched_16bit_convolution_default_choice(gpu_ctx, orc, pkg):
+    """Batched 16-bit 3x3 convolutions through the automatic kernel choice:
+    enough tiles for the many-tile rule, which takes the 64 x 128
+    channel-last tile at stride 1; every output element against the float64
+    convolution."""
+    I = pkg.inputs
+    cases = [((128, 32, 32, 32), (64, 32, 3, 3), 1, 1, "conv_cl_f16_3x3s1_64x128w1")]
+    for i, (xs, ws, s, p, want) in enumerate(cases):
+        x = round_in(I.uniform(2900 + i, xs, -1, 1), "float16")
+        w = round_in(I.uniform(2910 + i, ws, -0.5, 0.5), "float16")
+        b = round_in(I.uniform(2920 + i, (ws[0],), -0.5, 0.5), "float16")
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), 1)
+        got, kernel = run_conv(gpu_ctx, x, w, b, "float16", (s, s), (p, p), out_shape=list(ref.shape))
+        assert kernel == want, kernel
+        assert_parity(got, ref, refa, "float16", ws[1] * 9, f"batched {i} {xs}x{ws} s{s} {kernel}")
+
+
 @pytest.mark.parametrize("rv", ["1", "0"])
 @pytest.mark.parametrize("cfg", ["1x2w4", "2x1w2", "1x1w1", "2x2w8"])
 def test_lds_patch_float32_eight_channel_chunks(gpu_ctx, orc, pkg, monkeypatch, cfg, rv):

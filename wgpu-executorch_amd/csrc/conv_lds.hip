@@ -508,9 +508,19 @@ struct GeoCL {
   // a*S + kh start row(kh) after row a*S (r / S steps by kh / S), and column
   // b*S + kw sits slot(kw) after slot b*S
   static constexpr int toff(int t) { return row(t / KW) + slot(t % KW) * 32; }
+  // row-segment staging: 8-column segments of one channel (16 bytes), at
+  // most NSEG per patch row (the first one starts up to 7 columns left of
+  // the patch), one task per (row, segment, half of the chunk's channels)
+  static constexpr int NSEG = (PW + 7 + 7) / 8;
+  static constexpr int NTASK = PH * NSEG * 2;
+  static constexpr int NPASS = (NTASK + 63) / 64;
 };
 
-template <int DT, int KH, int KW, int S, int TM, int TN>
+// RV: the patch loaded as 16-byte row segments (images whose width is a
+// multiple of 8 columns): a lane loads one segment of each of 8 channels and
+// turns the 8 x 8 block channel-last in registers, 16 bytes per pixel, in
+// place of one 2-byte load per pixel and channel.
+template <int DT, int KH, int KW, int S, int TM, int TN, bool RV>
 __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p) {
   using G = GeoCL<KH, KW, S, TN>;
   constexpr int T = G::T, NBLK = G::NBLK;
@@ -547,15 +557,42 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
   // (OOB outside the image) and its LDS slot (-1 past the patch)
   const int ih0 = oh0 * S - p.pH, iw0 = ow0 * S - p.pW;
   const int plane = p.IH * p.IW;
-  uint32_t vp[NBLK];
-  int vw[NBLK];
+  constexpr int NP = RV ? 1 : NBLK;
+  uint32_t vp[NP];
+  int vw[NP];
+  if constexpr (!RV) {
 #pragma unroll
-  for (int e = 0; e < NBLK; ++e) {
-    const int q = e * 64 + lane;
-    const int pr = q / G::PW, pc = q - pr * G::PW;
-    const int ih = ih0 + pr, iw = iw0 + pc;
-    vp[e] = (q < G::PHW && ih >= 0 && ih < p.IH && iw >= 0 && iw < p.IW) ? (uint32_t)(ih * p.IW + iw) * 2 : OOB;
-    vw[e] = q < G::PHW ? G::row(pr) + G::slot(pc) * 32 : -1;
+    for (int e = 0; e < NBLK; ++e) {
+      const int q = e * 64 + lane;
+      const int pr = q / G::PW, pc = q - pr * G::PW;
+      const int ih = ih0 + pr, iw = iw0 + pc;
+      vp[e] = (q < G::PHW && ih >= 0 && ih < p.IH && iw >= 0 && iw < p.IW) ? (uint32_t)(ih * p.IW + iw) * 2 : OOB;
+      vw[e] = q < G::PHW ? G::row(pr) + G::slot(pc) * 32 : -1;
+    }
+  }
+  // RV task q = e*64 + lane: channel half q & 1, patch row r = (q/2) / NSEG,
+  // segment g = (q/2) % NSEG at image column a0 + 8g (a0: iw0 rounded down
+  // to a multiple of 8, so a segment lies wholly inside or outside the
+  // image); sp: its input offset in channel 0 of the chunk (OOB outside),
+  // sr: LDS offset of its row and channel half (-1: no task), sg: the patch
+  // column of its first pixel
+  constexpr int NS = RV ? G::NPASS : 1;
+  uint32_t sp[NS];
+  int sr[NS], sg[NS];
+  if constexpr (RV) {
+    const int a0 = iw0 - (((iw0 % 8) + 8) % 8), dl = iw0 - a0;
+#pragma unroll
+    for (int e = 0; e < G::NPASS; ++e) {
+      const int q = e * 64 + lane, h = q & 1, rs = q >> 1;
+      const int r = rs / G::NSEG, g = rs - r * G::NSEG;
+      const int ih = ih0 + r, s0 = a0 + 8 * g;
+      const bool ok = q < G::NTASK;
+      sp[e] = (ok && ih >= 0 && ih < p.IH && s0 >= 0 && s0 < p.IW)
+                  ? (uint32_t)((ih * p.IW + s0) * 2 + h * 8 * plane * 2)
+                  : OOB;
+      sr[e] = ok ? G::row(r) + h * 16 : -1;
+      sg[e] = 8 * g - dl;
+    }
   }
   char* wl = lds + wave * G::LDS_WAVE;
   float brow[TM];
@@ -584,24 +621,53 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   // the chunk's patch pixels in registers, channels 2m and 2m+1 in pv[e][m]
-  uint32_t pv[NBLK][8];
+  // (RV: segment e of channel ch in ps[e][ch], pixels 2d and 2d+1 in dword d)
+  uint32_t pv[RV ? 1 : NBLK][8];
+  uint4 ps[NS][RV ? 8 : 1];
   auto load_patch = [&](int c) {
     const rsrc_t rx = rsrc(ximg + (long long)c * chunk_x, chunk_x);
+    if constexpr (RV) {
 #pragma unroll
-    for (int e = 0; e < NBLK; ++e)
+      for (int e = 0; e < G::NPASS; ++e)
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const uint32_t lo = ld_el<2>(rx, vp[e], 2 * m * cplane), hi = ld_el<2>(rx, vp[e], (2 * m + 1) * cplane);
-        pv[e][m] = lo | (hi << 16);
-      }
+        for (int ch = 0; ch < 8; ++ch) ps[e][ch] = ld16(rx, sp[e], ch * cplane);
+    } else {
+#pragma unroll
+      for (int e = 0; e < NBLK; ++e)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          const uint32_t lo = ld_el<2>(rx, vp[e], 2 * m * cplane), hi = ld_el<2>(rx, vp[e], (2 * m + 1) * cplane);
+          pv[e][m] = lo | (hi << 16);
+        }
+    }
   };
   auto store_patch = [&]() {
+    if constexpr (RV) {
+      auto dw = [](const uint4& v, int d) { return d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w; };
 #pragma unroll
-    for (int e = 0; e < NBLK; ++e)
-      if (vw[e] >= 0) {
-        *reinterpret_cast<uint4*>(wl + vw[e]) = make_uint4(pv[e][0], pv[e][1], pv[e][2], pv[e][3]);
-        *reinterpret_cast<uint4*>(wl + vw[e] + 16) = make_uint4(pv[e][4], pv[e][5], pv[e][6], pv[e][7]);
-      }
+      for (int e = 0; e < G::NPASS; ++e)
+        if (sr[e] >= 0) {
+#pragma unroll
+          for (int px = 0; px < 8; ++px) {
+            const int col = sg[e] + px;
+            if (col < 0 || col >= G::PW) continue;
+            uint32_t m4[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const uint32_t a = dw(ps[e][2 * m], px >> 1), b = dw(ps[e][2 * m + 1], px >> 1);
+              m4[m] = (px & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+            }
+            *reinterpret_cast<uint4*>(wl + sr[e] + G::slot(col) * 32) = make_uint4(m4[0], m4[1], m4[2], m4[3]);
+          }
+        }
+    } else {
+#pragma unroll
+      for (int e = 0; e < NBLK; ++e)
+        if (vw[e] >= 0) {
+          *reinterpret_cast<uint4*>(wl + vw[e]) = make_uint4(pv[e][0], pv[e][1], pv[e][2], pv[e][3]);
+          *reinterpret_cast<uint4*>(wl + vw[e] + 16) = make_uint4(pv[e][4], pv[e][5], pv[e][6], pv[e][7]);
+        }
+    }
   };
   // the lane's raw weight run of the next chunk (element c*T + t: channel c,
   // tap t) and the fragments of the current one
@@ -681,7 +747,7 @@ struct Cfg {
 template <bool CL, bool RV, int DT, int KH, int KW, int S, int TM, int TN>
 hipError_t launch_t(const CParams& p, size_t lds, unsigned grid, int w, hipStream_t s) {
   void (*fn)(CParams);
-  if constexpr (CL) fn = k_conv_cl<DT, KH, KW, S, TM, TN>;
+  if constexpr (CL) fn = k_conv_cl<DT, KH, KW, S, TM, TN, RV>;
   else fn = k_conv_lds<DT, KH, KW, S, TM, TN, RV>;
   // the channel-last kernel's larger tiles are built for at most 256 threads
   if (CL && TM * TN >= 4 && w > 4) return hipErrorInvalidValue;
@@ -714,7 +780,9 @@ template <bool CL, bool RV, int DT, int KH, int KW, int S>
 hipError_t launch_geo(const CParams& p, const Cfg& c, unsigned grid, hipStream_t s) {
   if (c.tm == 1 && c.tn == 1) return launch_cfg<CL, RV, DT, KH, KW, S, 1, 1>(p, c, grid, s);
   if (c.tm == 1 && c.tn == 2) return launch_cfg<CL, RV, DT, KH, KW, S, 1, 2>(p, c, grid, s);
-  if (c.tm == 2 && c.tn == 1) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 1>(p, c, grid, s);
+  // (the channel-last 64 x 32 tile with row segments would spill: not built)
+  if constexpr (!(CL && RV))
+    if (c.tm == 2 && c.tn == 1) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 1>(p, c, grid, s);
   if (c.tm == 2 && c.tn == 2) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 2>(p, c, grid, s);
   if constexpr (S == 1)
     if (c.tm == 2 && c.tn == 4) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 4>(p, c, grid, s);
@@ -728,6 +796,8 @@ hipError_t launch_dt(const CParams& p, const Cfg& c, int S, unsigned grid, hipSt
       return S == 1 ? launch_geo<false, true, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, true, DT, 3, 3, 2>(p, c, grid, s);
     return S == 1 ? launch_geo<false, false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, false, DT, 3, 3, 2>(p, c, grid, s);
   } else {
+    if (c.cl && c.rv)
+      return S == 1 ? launch_geo<true, true, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<true, true, DT, 3, 3, 2>(p, c, grid, s);
     if (c.cl) return S == 1 ? launch_geo<true, false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<true, false, DT, 3, 3, 2>(p, c, grid, s);
     return S == 1 ? launch_geo<false, false, DT, 3, 3, 1>(p, c, grid, s) : launch_geo<false, false, DT, 3, 3, 2>(p, c, grid, s);
   }
@@ -748,13 +818,27 @@ long long tile_count(const ConvLdsDesc& d, const Cfg& c) {
 //    64 tile (64 x 32 for 16-bit data at stride 2, whose patch is larger) and
 //    W waves per block splitting its chunks of input channels, W up to the chunk
 //    count and 8 while the waves stay below four per SIMD;
-//  - many tiles: 64 x 64, one wave per tile, float32 only.  For 16-bit data
-//    the LDS-staged GEMM (gemm_mfma's 128 x 256 conv form) is faster there,
-//    and choose() returns tm = 0: the kernel does not apply.
+//  - many tiles: 64 x 64, one wave per tile, for float32; for 16-bit data at
+//    stride 1 on images whose rows are whole 16-byte segments, the 64 x 128
+//    channel-last tile; for other 16-bit shapes the LDS-staged GEMM
+//    (gemm_mfma's conv form) is faster, and choose() returns tm = 0: the
+//    kernel does not apply.
 // WGX_CONV_LDS=TMxTNwW forces a configuration.
 Cfg choose(const ConvLdsDesc& d, int cus) {
   const long long simds = 4LL * cus;
   const bool cl = d.dtype != WGX_FLOAT32 && !(getenv("WGX_CONV_CL") && strcmp(getenv("WGX_CONV_CL"), "0") == 0);
+  // many tiles, 16-bit: the 64 x 128 channel-last tile with row-segment patch
+  // loads at stride 1 while it still gives every SIMD a wave ([16,64,80,80]
+  // -> 128: 60.9 us, [64,64,80,80]: 199 us, [8,32,160,160] -> 64: 45.9 us,
+  // against 68.9 / 222 / 64.5 us for the LDS-staged GEMM); otherwise the GEMM
+  // ([16,128,40,40] -> 256: 46.7 us against 56.8 for 32 x 64 one-wave tiles)
+  auto many16 = [&]() {
+    const bool seg = cl && d.IW % 8 == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
+                     !(getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0);
+    Cfg m{2, 4, 1, cl};
+    if (!(seg && d.sH == 1 && tile_count(d, m) >= simds)) m.tm = 0;
+    return m;
+  };
   Cfg c{2, 2, 1, cl};
   if (tile_count(d, c) < 2 * simds) {
     if (d.dtype != WGX_FLOAT32 && d.sH == 2) c = Cfg{2, 1, 1, cl};
@@ -765,8 +849,11 @@ Cfg choose(const ConvLdsDesc& d, int cus) {
     // 16-bit chunk): [1,64,80,80] float32 16.8 us at 4 waves, 17.3 at 8
     while (w < 8 && w * 32 <= d.IC && tiles * w * 2 <= 4 * simds) w *= 2;
     c.w = w;
+    // one wave per tile because the tiles are many (not because the input
+    // has a single 16-channel chunk): the many-tile choice
+    if (d.dtype != WGX_FLOAT32 && w == 1 && d.IC >= 32 && tiles * 2 > 4 * simds) c = many16();
   } else if (d.dtype != WGX_FLOAT32) {
-    c.tm = 0;
+    c = many16();
   }
   if (const char* e = getenv("WGX_CONV_LDS")) {
     int tm = 0, tn = 0, ww = 0;
@@ -795,11 +882,12 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   if (!conv_lds_applies(d)) return hipErrorNotSupported;
   Cfg c = choose(d, cus);
   if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
-  // float32 images whose width is a multiple of 4 columns (16-byte rows on a
-  // 16-byte base) load the patch as row segments; WGX_CONV_RV=0 keeps the
-  // element loads
-  c.rv = d.dtype == WGX_FLOAT32 && d.IW % 4 == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
-         !(getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0);
+  // images whose rows are whole 16-byte segments on a 16-byte base (float32:
+  // a multiple of 4 columns, 16-bit: of 8) load the patch as row segments;
+  // WGX_CONV_RV=0 keeps the element loads
+  const bool rv_off = getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0;
+  c.rv = d.IW % (d.dtype == WGX_FLOAT32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
+         (d.dtype == WGX_FLOAT32 || (c.cl && !(c.tm == 2 && c.tn == 1))) && !rv_off;
   CParams p{};
   p.x = d.x;
   p.w = d.w;

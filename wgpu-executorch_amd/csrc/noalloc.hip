@@ -35,7 +35,10 @@ hipError_t noalloc_scratch(int device, void** out) {
     void* p = nullptr;
     if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e == hipSuccess && p == nullptr) e = hipErrorInvalidSymbol;
-    if (cur >= 0 && cur != device) hipSetDevice(cur);
+    if (cur >= 0 && cur != device) {
+      const hipError_t r = hipSetDevice(cur);  // the caller's device back
+      if (e == hipSuccess) e = r;
+    }
     g_ptr[device] = e == hipSuccess ? p : nullptr;
     g_err[device] = e;
     g_done[device] = true;
