@@ -528,6 +528,8 @@ def main():
                     help="record one configuration and submit it a few times (for rocprofv3 --pmc runs)")
     ap.add_argument("--gemm-k-sweep", action="store_true",
                     help="time the fp16 addmm NT form at M=4096, N=3072 for K = 64 ... 3072 (amortised) and exit")
+    ap.add_argument("--yolo26n-only", action="store_true",
+                    help="run only the reference's yolo26n float16 program (ms/frame) and exit")
     ap.add_argument("--vendor-probe", action="store_true",
                     help=argparse.SUPPRESS)  # the child run that times the vendor kernels
     ap.add_argument("--traffic-probe", choices=list(CONV2), default=None,
@@ -537,6 +539,10 @@ def main():
         # torch ships its own HIP runtime: it runs in a process of its own,
         # one that never loads libwgx
         print(json.dumps(vendor_configs()), flush=True)
+        return
+    if args.yolo26n_only:
+        # the frame runs in a Node child process; this one never touches the GPU
+        print(json.dumps({"5_yolo26n_f16": yolo26n_frame(args.quick)}), flush=True)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on exactly one GPU (the hot path is not sharded); "

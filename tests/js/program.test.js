@@ -169,6 +169,34 @@ describe('recordProgram views', () => {
     deep.values[5] = S(-2);
     expect(elidedOf(deep)).toEqual([2]);
   });
+  it('ties flat copies: clone without a memory format, squeeze_copy, unsqueeze_copy', () => {
+    // t = x + x -> c = clone(t) -> s = squeeze_copy(c, [0]) -> u = unsqueeze_copy(s, 0)
+    // -> out = u + u; then the same with a memory format on the clone
+    const flat = (memfmt) => ({
+      version: '1',
+      chain: [
+        add(0, 0, 1, 2),
+        { name: 'aten.clone.default', args: [2, 3, 4] },
+        { name: 'aten.squeeze_copy.dims', args: [4, 5, 6] },
+        { name: 'aten.unsqueeze_copy.default', args: [6, 7, 8] },
+        add(8, 8, 1, 9),
+      ],
+      values: [
+        T([1, 4, 2, 2], { memObjId: 0 }), S(1), T([1, 4, 2, 2], { memObjId: 1 }),
+        memfmt ? S(memfmt) : { type: 'null' }, T([1, 4, 2, 2], { memObjId: 2 }),
+        L([0]), T([4, 2, 2], { memObjId: 1 }), S(0), T([1, 4, 2, 2], { memObjId: 2 }),
+        T([1, 4, 2, 2], { memObjId: 3 }),
+      ],
+      inputIds: [0],
+      outputIds: [9],
+      memoryPlan: { pools: [0, 1, 2, 3].map((id) => ({ id, size: 64 })) },
+    });
+    const p = flat(null);
+    expect(elidedOf(p)).toEqual([1, 2, 3]);
+    const plan = W._planViews(p);
+    for (const id of [4, 6, 8]) expect(plan.place.get(id).off - plan.place.get(2).off).toEqual(0);
+    expect(elidedOf(flat(2))).toEqual([2, 3]);
+  });
   // o1 = a + b, o2 = a * b, o3 = o1 + o2, all three program outputs
   const threeOut = () => ({
     version: '1',

@@ -658,10 +658,11 @@ function siluTriples(program) {
 }
 
 /**
- * Zero-copy concatenation, split and view_copy.  When every dimension
+ * Zero-copy concatenation, split and flat copies.  When every dimension
  * before the cat (split) dimension has size 1, a concatenation is its inputs
  * laid end to end and each piece of a split is a contiguous byte range of
- * its input; a view_copy is its input's bytes unchanged.  If the producers of
+ * its input; a view_copy, squeeze_copy, unsqueeze_copy or clone (without a
+ * memory format) is its input's bytes unchanged.  If the producers of
  * the pieces write straight into the whole, such an op has nothing left to
  * do.  Each op ties its tensors together at fixed byte offsets (a union-find
  * with offsets); tied tensors form a group that gets memory of its own,
@@ -674,6 +675,11 @@ function siluTriples(program) {
  * Returns place: value -> {root, off} (byte offset within the group),
  * groupBytes: root -> group size, elided: chain indices with nothing to do.
  */
+// Copies whose output is their input's bytes unchanged (a clone without a
+// memory format; the shape-only copies).
+const FLAT_COPIES = new Set(['aten.view_copy.default', 'aten.clone.default', 'aten.squeeze_copy.dims',
+  'aten.unsqueeze_copy.default']);
+
 function planViews(program) {
   const { chain, values } = program;
   const producer = new Map();
@@ -756,7 +762,8 @@ function planViews(program) {
       const items = values[a[3]].items, x = a[0];
       const offs = contiguousPieces(x, items, values[a[2]].value);
       if (offs) ties = items.map((id, i) => [id, x, offs[i]]);
-    } else if (op.name === 'aten.view_copy.default' && a.length === 3) {
+    } else if (FLAT_COPIES.has(op.name) && a.length === 3 &&
+               (op.name !== 'aten.clone.default' || !values[a[1]] || values[a[1]].type === 'null')) {
       const x = a[0], y = a[2];
       if (values[x] && values[y] && values[x].type === 'tensor' && values[y].type === 'tensor' &&
           values[x].dtype === values[y].dtype && valueBytes(values[x]) === valueBytes(values[y])) ties = [[y, x, 0]];
