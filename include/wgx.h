@@ -193,8 +193,10 @@ int wgx_record_conv2d(wgx_ctx* ctx, const wgx_tensor* in, const wgx_tensor* weig
  * counterpart in the reference: recordProgram folds
  * aten.add.Tensor(a, b, alpha) into the convolution that produces a or b
  * with it (src/shaders/add/index.ts:33-129: out = a + alpha * b).  Depthwise
- * convolutions only; residual may be the output itself but must not
- * partly overlap it. */
+ * convolutions, and dense 3x3 convolutions (stride 1 or 2, dilation 1, a
+ * multiple of 8 float32 or 16 16-bit input channels) that the LDS-patch
+ * kernel takes; WGX_ERR_INVALID for the rest.  residual may be the output
+ * itself but must not partly overlap it. */
 int wgx_record_conv2d_residual(wgx_ctx* ctx, const wgx_tensor* in, const wgx_tensor* weight,
                                const wgx_tensor* bias, const wgx_conv_args* args,
                                const wgx_tensor* residual, float conv_scale,

@@ -235,8 +235,9 @@ def test_im2col_table_matches_oracle_indexing(pkg, orc):
 
 
 def test_conv_residual_validation(hctx, pkg):
-    """The residual epilogue's checks: depthwise only, the output's shape and
-    dtype, the output itself or no overlap at all."""
+    """The residual epilogue's checks: depthwise convolutions and the dense
+    3x3 ones the LDS-patch kernel takes, the output's shape and dtype, the
+    output itself or no overlap at all."""
     E = pkg.wgx.WgxError
     T = hctx.tensor
     x, w, b = T("float16", [1, 8, 10, 10]), T("float16", [8, 1, 3, 3]), T("float16", [8])
@@ -244,8 +245,16 @@ def test_conv_residual_validation(hctx, pkg):
     hctx.convolution(x, w, b, 1, 1, 1, False, 0, 8, y, residual=r, residual_scale=0.5)
     assert hctx.last_kernel.startswith("depthwise_f16_3x3s1")
     hctx.convolution(x, w, b, 1, 1, 1, False, 0, 8, y, residual=y)  # in place
-    with pytest.raises(E, match="depthwise convolutions only"):
+    # a dense 3x3 convolution over 8 input channels: no LDS-patch kernel (16-bit
+    # chunks are 16 channels), so no residual epilogue
+    with pytest.raises(E, match="the LDS-patch kernel takes"):
         hctx.convolution(x, T("float16", [8, 8, 3, 3]), b, 1, 1, 1, False, 0, 1, y, residual=r)
+    # over 16: the channel-last LDS-patch kernel adds it
+    x16 = T("float16", [1, 16, 10, 10])
+    hctx.convolution(x16, T("float16", [8, 16, 3, 3]), b, 1, 1, 1, False, 0, 1, y, residual=r)
+    assert hctx.last_kernel.startswith("conv_cl_f16_3x3s1")
+    with pytest.raises(E, match="the LDS-patch kernel takes"):
+        hctx.convolution(x16, T("float16", [8, 16, 1, 1]), b, 1, 0, 1, False, 0, 1, y, residual=r)
     with pytest.raises(E, match="match the output"):
         hctx.convolution(x, w, b, 1, 1, 1, False, 0, 8, y, residual=T("float16", [1, 8, 10, 11]))
     with pytest.raises(E, match="match the output"):

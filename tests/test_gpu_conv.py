@@ -358,6 +358,51 @@ RESIDUAL_CASES = [
 ]
 
 
+DENSE_RESIDUAL_CASES = [
+    # x shape, w shape, stride, pad, (conv scale, residual scale), in place, forced configuration
+    ((1, 32, 20, 24), (48, 32, 3, 3), 1, 1, (1.0, 1.0), False, None),
+    ((2, 64, 16, 16), (40, 64, 3, 3), 2, 1, (0.5, -1.0), False, None),
+    ((1, 64, 24, 24), (64, 64, 3, 3), 1, 1, (1.0, 1.0), True, None),      # residual is the output
+    ((1, 32, 17, 13), (24, 32, 3, 3), 1, 1, (1.0, 2.0), False, "2x2w4"),  # W > 1, ragged edges
+    ((2, 32, 16, 32), (64, 32, 3, 3), 1, 1, (1.0, 1.0), True, "2x4w1"),   # the 64 x 128 tile, in place
+]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_dense_conv_silu_residual_epilogue(gpu_ctx, orc, pkg, monkeypatch, dtype):
+    """Dense 3x3 convolution + SiLU + an output-shaped residual in one launch
+    of the LDS-patch kernel (channel-major float32, channel-last 16-bit),
+    out = cs * silu(conv) + rs * residual, including a residual that is the
+    output itself, against the fp64 oracle."""
+    W, I = pkg.wgx, pkg.inputs
+    for i, (xs, ws, s, p, (cs, rs), inplace, cfg) in enumerate(DENSE_RESIDUAL_CASES):
+        if cfg is not None:
+            if dtype == "float32" and cfg == "2x4w1":
+                continue  # the 64 x 128 tile is 16-bit only
+            monkeypatch.setenv("WGX_CONV_LDS", cfg)
+        else:
+            monkeypatch.delenv("WGX_CONV_LDS", raising=False)
+        x = round_in(I.uniform(2400 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(2410 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(2420 + i, (ws[0],), -0.5, 0.5), dtype)
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), 1)
+        r = round_in(I.uniform(2430 + i, ref.shape, -2, 2), dtype)
+        tx, tw, tb = gpu_ctx.from_numpy(x, dtype), gpu_ctx.from_numpy(w, dtype), gpu_ctx.from_numpy(b, dtype)
+        tr = gpu_ctx.from_numpy(r, dtype)
+        ty = tr if inplace else gpu_ctx.tensor(dtype, list(ref.shape))
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], 1, ty,
+                            activation=W.ACT_SILU, residual=tr, conv_scale=cs, residual_scale=rs)
+        kernel = gpu_ctx.last_kernel
+        assert kernel.startswith("conv_lds_" if dtype == "float32" else "conv_cl_"), kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        want = cs * (ref / (1.0 + np.exp(-ref))) + rs * r.astype(np.float64)
+        bound = 1.1 * abs(cs) * refa + abs(rs) * np.abs(r.astype(np.float64))
+        assert_parity(ty.get_f32(), want, bound, dtype, ws[1] * 9,
+                      f"dense residual {i} {dtype} {xs}x{ws} s{s} {kernel}")
+
+
 @pytest.mark.parametrize("dtype", ["float32", "float16"])
 def test_depthwise_silu_residual_epilogue(gpu_ctx, orc, pkg, dtype):
     """Depthwise convolution + SiLU + an output-shaped residual in one launch,

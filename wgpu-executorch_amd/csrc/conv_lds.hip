@@ -83,6 +83,8 @@ struct CParams {
   int W;        // waves per block sharing one tile
   int act, has_clamp;
   float cmin, cmax;
+  const void* res;  // output-shaped residual or null: y = rcs * y + rrs * res
+  float rcs, rrs;
 };
 
 template <int DT>
@@ -197,14 +199,36 @@ __device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM
     for (int ii = 0; ii < TM; ++ii)
       if (ii == i) bias = brow[ii];
     float vv[4] = {v.x + bias, v.y + bias, v.z + bias, v.w + bias};
+    const long long eo = (long long)oc * p.OH * p.OW + (long long)oh * p.OW + ow;
+    char* dst = yimg + eo * ES;
+    // the residual's elements at the output's positions, read by the lane
+    // that writes them (a residual that is the output itself is fine)
+    uint32_t rr[4] = {0u, 0u, 0u, 0u};
+    if (p.res) {
+      const char* rsrc_p = static_cast<const char*>(p.res) + ((long long)z * p.sy + eo) * ES;
+      if (vec && ow + 3 < p.OW) {
+        if constexpr (ES == 4) {
+          const uint4 t = *reinterpret_cast<const uint4*>(rsrc_p);
+          rr[0] = t.x, rr[1] = t.y, rr[2] = t.z, rr[3] = t.w;
+        } else {
+          const uint2 t = *reinterpret_cast<const uint2*>(rsrc_p);
+          rr[0] = t.x & 0xffffu, rr[1] = t.x >> 16, rr[2] = t.y & 0xffffu, rr[3] = t.y >> 16;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (ow + e < p.OW)
+            rr[e] = ES == 4 ? reinterpret_cast<const uint32_t*>(rsrc_p)[e] : reinterpret_cast<const uint16_t*>(rsrc_p)[e];
+      }
+    }
     uint32_t h[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float x = apply_act(p.act, vv[e]);
       if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
+      if (p.res) x = p.rcs * x + p.rrs * to_f<DT>(rr[e]);
       h[e] = from_f<DT>(x);
     }
-    char* dst = yimg + ((long long)oc * p.OH * p.OW + (long long)oh * p.OW + ow) * ES;
     if (vec && ow + 3 < p.OW) {
       if constexpr (ES == 4) *reinterpret_cast<uint4*>(dst) = make_uint4(h[0], h[1], h[2], h[3]);
       else *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
@@ -913,6 +937,9 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   p.has_clamp = d.has_clamp;
   p.cmin = d.cmin;
   p.cmax = d.cmax;
+  p.res = d.res;
+  p.rcs = d.res_conv_scale;
+  p.rrs = d.res_scale;
   if (name) {
     char buf[96];
     snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d", c.cl ? "cl" : "lds",

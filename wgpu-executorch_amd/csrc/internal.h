@@ -102,6 +102,10 @@ struct ConvLdsDesc {
   int act;  // WGX_ACT_*: applied after the bias, before the clamp
   int has_clamp;
   float cmin, cmax;
+  // optional residual of the output's shape, added after the clamp:
+  // y = res_conv_scale * y + res_scale * res (null: none)
+  const void* res;
+  float res_conv_scale, res_scale;
 };
 bool conv_lds_applies(const ConvLdsDesc& d);
 // cus: compute units of the device (the configuration depends on it)

@@ -696,10 +696,9 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
     if (e == hipSuccess) return c->push([d](hipStream_t s) { return launch_depthwise(d, s, nullptr); }, name);
     // bands too wide for LDS: fall through to the direct kernel
   }
-  if (res)
-    return c->fail(WGX_ERR_INVALID, "convolution: a residual is supported on depthwise convolutions only");
   // dense 3x3 convolutions over a multiple of 8 (float32) or 16 input channels: the
-  // LDS-patch implicit GEMM (no per-element address work)
+  // LDS-patch implicit GEMM (no per-element address work), the one dense
+  // kernel with the residual epilogue
   if (!args->transposed && groups == 1 && dH == 1 && dW == 1) {
     ConvLdsDesc ld{};
     ld.dtype = dt;
@@ -724,6 +723,9 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
     ld.has_clamp = has_clamp;
     ld.cmin = cmin;
     ld.cmax = cmax;
+    ld.res = res ? res->data : nullptr;
+    ld.res_conv_scale = rcs;
+    ld.res_scale = rrs;
     if (conv_lds_applies(ld)) {
       const int cus = device_cu_count(c);
       e = launch_conv_lds(ld, cus, c->dry(), &name);
@@ -734,6 +736,10 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
       // that the GEMM kernels below run faster
     }
   }
+  if (res)
+    return c->fail(WGX_ERR_INVALID,
+                   "convolution: a residual is supported on depthwise convolutions and on the dense 3x3 "
+                   "convolutions the LDS-patch kernel takes");
   const ConvGeom geom{(int)IH, (int)IW, (int)OW, sH, sW, pH, pW, (int)KH, (int)KW, dH, dW};
   // A 1x1 convolution is a plain GEMM with the input plane as its [IC, H*W]
   // operand -- unless it has fewer 64 x 64 output tiles than CUs: then it

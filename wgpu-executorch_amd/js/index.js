@@ -407,7 +407,7 @@ class WgpuExecutionContext {
         fargs.pop();
         if (t.add) {
           fargs.push(tensors.get(t.add.r), t.add.convScale, t.add.residualScale, tensors.get(t.add.z));
-          fused.set(t.k, { shader: shaders.convolutionSiluAdd, args: fargs, ops: 4 });
+          fused.set(t.k, { shader: shaders.convolutionSiluAdd, args: fargs, ops: 4, y: t.y });
         } else {
           fargs.push(tensors.get(t.y));
           fused.set(t.k, { shader: shaders.convolutionSilu, args: fargs, ops: 3 });
@@ -428,7 +428,33 @@ class WgpuExecutionContext {
       if (views.elided.has(k)) continue;  // its output already is its inputs' bytes
       const f = fused.get(k);
       if (f !== undefined) {  // conv -> sigmoid -> mul (-> add) as one convolution launch
-        this.recordShader(f.shader, f.args);
+        if (f.ops === 4) {
+          try {
+            this.recordShader(f.shader, f.args);
+          } catch (e) {
+            // a convolution whose kernel has no residual epilogue: conv+SiLU
+            // into the product, then the add as an op of its own -- or, when
+            // the memory plan gives the product the space of something the
+            // convolution reads (the unfused chain writes it only later), the
+            // four ops as they stand
+            if (!/residual is supported/.test(e.message)) throw e;
+            const ty = tensors.get(f.y);
+            if (convReads(program, k, tensors).some((r) => overlaps(r, ty))) {
+              for (let q = k; q < k + 3; q++) {
+                const op = program.chain[q];
+                this.recordShader(shaderRegistry[op.name], resolveArgs(op, program.values, tensors));
+              }
+            } else {
+              const sargs = f.args.slice(0, 9);
+              sargs.push(ty);
+              this.recordShader(shaders.convolutionSilu, sargs);
+            }
+            const addOp = program.chain[k + 3];
+            this.recordShader(shaderRegistry[addOp.name], resolveArgs(addOp, program.values, tensors));
+          }
+        } else {
+          this.recordShader(f.shader, f.args);
+        }
         k += f.ops - 1;
         continue;
       }
@@ -613,11 +639,13 @@ function convReads(program, k, tensors) {
  * read by nothing else (and are not program outputs) the convolution can
  * write SiLU(conv) straight into y, one launch instead of three and two
  * feature-map round trips fewer.  When the next op is aten.add.Tensor with y
- * as one operand (and y read by nothing else) on a depthwise convolution, the
- * add joins too: the depthwise kernels add an output-shaped residual in their
- * epilogue.  Returns {k, y, add}: k the convolution's chain index, y the
- * product, add null or {k, r, z, convScale, residualScale} with z = the add's
- * output = convScale * y + residualScale * r.
+ * as one operand (and y read by nothing else), the add joins too: the
+ * depthwise kernels and the dense LDS-patch kernel add an output-shaped
+ * residual in their epilogue (a convolution that another kernel runs is
+ * recorded as conv+SiLU and the add, see recordProgram).  Returns {k, y,
+ * add}: k the convolution's chain index, y the product, add null or {k, r, z,
+ * convScale, residualScale} with z = the add's output = convScale * y +
+ * residualScale * r.
  */
 function siluTriples(program) {
   const { chain, values } = program;
@@ -634,19 +662,15 @@ function siluTriples(program) {
     if (uses.get(c) !== 3 || uses.get(s) !== 2 || !same(values[c], values[y])) continue;
     const t = { k, y, add: null };
     // aten.add.Tensor(a, b, alpha) -> z right after, with y one operand and
-    // read by nothing else, on a depthwise convolution: the residual epilogue
+    // read by nothing else: the residual epilogue
     const add = chain[k + 3];
     if (add && add.name === 'aten.add.Tensor' && add.args.length === 4 && uses.get(y) === 2 &&
         (add.args[0] === y) !== (add.args[1] === y)) {
       const r = add.args[0] === y ? add.args[1] : add.args[0];
       const av = values[add.args[2]];
       const alpha = av && av.type === 'scalar' ? Number(av.value) : 1;
-      const w = values[conv.args[1]], xin = values[conv.args[0]];
-      const groups = values[conv.args[8]] && values[conv.args[8]].type === 'scalar' ? values[conv.args[8]].value : 1;
       const transposed = values[conv.args[6]] && values[conv.args[6]].value;
-      const depthwise = !transposed && w && xin && w.shape.length === 4 && xin.shape.length === 4 &&
-        w.shape[1] === 1 && w.shape[0] === groups && xin.shape[1] === groups;
-      if (depthwise && Number.isFinite(alpha) && same(values[r], values[y]) && same(values[add.args[3]], values[y])) {
+      if (!transposed && Number.isFinite(alpha) && same(values[r], values[y]) && same(values[add.args[3]], values[y])) {
         t.add = { k: k + 3, r, z: add.args[3],
           convScale: add.args[1] === y ? alpha : 1, residualScale: add.args[1] === y ? 1 : alpha };
       }

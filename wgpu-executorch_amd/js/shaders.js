@@ -213,12 +213,13 @@ module.exports = function makeShaders({ native, DTYPE_BYTESIZE }) {
 
   /**
    * aten.convolution.default, SiLU, then aten.add.Tensor with an
-   * output-shaped tensor, in one launch (depthwise convolutions):
-   * out = convScale * silu(conv) + residualScale * residual.
+   * output-shaped tensor, in one launch (depthwise convolutions and the
+   * dense 3x3 ones the LDS-patch kernel takes; the native layer refuses the
+   * rest): out = convScale * silu(conv) + residualScale * residual.
    */
   const convolutionSiluAdd = {
     name: 'wgx.convolution_silu_add',
-    code: { depthwise: 'the depthwise kernels with the SiLU and residual epilogue' },
+    code: { all: 'the depthwise and LDS-patch convolution kernels with the SiLU and residual epilogue' },
     recordIn(ctx, args) {
       const [inTensor, weight, bias, stride, padding, dilation, transposed, outputPadding, groups, residual,
         convScale, residualScale, outTensor] = args;

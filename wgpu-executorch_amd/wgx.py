@@ -312,7 +312,8 @@ class Context:
                     groups=1, out: Optional[Tensor] = None, clamp=None, activation: int = ACT_NONE,
                     residual: Optional[Tensor] = None, conv_scale: float = 1.0,
                     residual_scale: float = 1.0) -> "Context":
-        """residual: out = conv_scale * conv + residual_scale * residual (depthwise only)."""
+        """residual: out = conv_scale * conv + residual_scale * residual (depthwise
+        convolutions and the dense 3x3 ones the LDS-patch kernel takes)."""
         def hw(v):
             v = list(v) if isinstance(v, (list, tuple)) else [v]
             if len(v) == 1:
