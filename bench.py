@@ -80,12 +80,14 @@ PROBE_REPS = 5
 
 
 def traffic_probe(W, I, v):
-    """Child run counted by rocprofv3: the headline's conv `v` (float32)
-    PROBE_REPS times, then a device copy of COPY_BYTES PROBE_REPS times (the
-    calibration)."""
+    """Child run counted by rocprofv3: the headline's conv `v` (float32; "pair":
+    2a and 2b recorded back to back, which the runtime runs as one paired
+    launch) PROBE_REPS times, then a device copy of COPY_BYTES PROBE_REPS
+    times (the calibration)."""
     ctx = W.Context(0)
     try:
-        build_conv(ctx, I, CONV2[v], "float32", 40)
+        for name in (("2a", "2b") if v == "pair" else (v,)):
+            build_conv(ctx, I, CONV2[name], "float32", 40 + 10 * (name == "2b"))
         ctx.set_graph_mode(False)
         for _ in range(PROBE_REPS):
             ctx.submit()
@@ -103,14 +105,17 @@ def traffic_probe(W, I, v):
 
 # One configuration, recorded once and submitted PROBE_REPS times without a
 # graph (one dispatch per launch): the child run that rocprofv3 --pmc counts.
-KERNEL_PROBES = ("conv2a_f32", "conv2b_f32", "conv2a_f16", "conv2a_f16_b64", "conv2b_f16_b64", "addmm_nt",
+KERNEL_PROBES = ("conv2a_f32", "conv2b_f32", "conv2ab_f32", "conv2a_f16", "conv2a_f16_b64", "conv2b_f16_b64", "addmm_nt",
                  "addmm_nn", "bmm", "dw3a", "dw3b", "dw3a_b256", "dw3b_b256")
 
 
 def kernel_probe(W, I, name):
     ctx = W.Context(0)
     try:
-        if name.startswith("conv"):
+        if name == "conv2ab_f32":  # 2a and 2b back to back: one paired launch
+            build_conv(ctx, I, CONV2["2a"], "float32", 40)
+            build_conv(ctx, I, CONV2["2b"], "float32", 50)
+        elif name.startswith("conv"):
             build_conv(ctx, I, CONV2[name[4:6]], "float32" if name.endswith("f32") else "float16", 40,
                        batch=64 if name.endswith("_b64") else 1)
         elif name.startswith("addmm"):
@@ -142,8 +147,9 @@ def kernel_probe(W, I, name):
 
 
 def measure_traffic(v):
-    """HBM bytes per step of the headline conv `v` (its convolution or GEMM
-    dispatch, plus the split-K reduction when there is one) from two
+    """HBM bytes per step of the headline conv `v` ("pair": the paired launch
+    of 2a and 2b; else its convolution or GEMM dispatch, plus the split-K
+    reduction when there is one) from two
     rocprofv3 --pmc runs
     (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by what the
     counter reads for a plain copy of COPY_BYTES (which moves exactly
@@ -532,7 +538,7 @@ def main():
                     help="run only the reference's yolo26n float16 program (ms/frame) and exit")
     ap.add_argument("--vendor-probe", action="store_true",
                     help=argparse.SUPPRESS)  # the child run that times the vendor kernels
-    ap.add_argument("--traffic-probe", choices=list(CONV2), default=None,
+    ap.add_argument("--traffic-probe", choices=list(CONV2) + ["pair"], default=None,
                     help=argparse.SUPPRESS)  # the child run that rocprofv3 counts
     args = ap.parse_args()
     if args.vendor_probe:
@@ -576,6 +582,9 @@ def main():
         ctx.submit()
     ctx.sync()
     el = time.perf_counter() - t0
+    # 2a and 2b read and write disjoint buffers: the runtime may run them as
+    # one paired launch (WGX_MERGE=0 keeps them apart)
+    paired = ctx.paired_launches > 0
     ctx.destroy()
     ms_step = el * 1e3 / args.steps
     step_flops = sum(conv_flops(c) for c in CONV2.values())
@@ -589,32 +598,57 @@ def main():
     #  warm: 20 launches of one instance (operands stay in L2 / MALL).
     per_kernel, warm = {}, {}
     reps_in_graph = 20
-    for v, c in CONV2.items():
+    if paired:
+        # the step is one paired launch of 2a and 2b: that launch is the
+        # dominant (only) kernel; warm: 20 pairs on one set of buffers,
+        # amortised: a graph of (2a, 2b) instances over >= 300 MB
         kctx = W.Context(0)
         try:
-            build_conv(kctx, I, c, "float32", 40, repeat=reps_in_graph)
-            warm[v] = time_ctx(kctx, 20) / reps_in_graph
+            for _ in range(reps_in_graph):
+                for v, c in CONV2.items():
+                    build_conv(kctx, I, c, "float32", 40 + 10 * (v == "2b"))
+            warm["pair"] = time_ctx(kctx, 20) / reps_in_graph
         finally:
             kctx.destroy()
-        n = int(300e6 / conv_bytes(c, 4)) + 1
-        _, _, per_kernel[v] = measure(W, lambda ctx, i, c=c: build_conv(ctx, I, c, "float32", 40 + 10 * i), n,
-                                      reps_shape=5, reps_amort=10)
-    dom = max(per_kernel, key=per_kernel.get)
+        pair_bytes = sum(conv_bytes(c, 4) for c in CONV2.values())
+
+        def build_pair(ctx, i):
+            for v, c in CONV2.items():
+                build_conv(ctx, I, c, "float32", 40 + 10 * i + 5 * (v == "2b"))
+        _, _, per_kernel["pair"] = measure(W, build_pair, int(300e6 / pair_bytes) + 1, reps_shape=5, reps_amort=10)
+        dom, flops_dom, bytes_dom = "pair", step_flops, pair_bytes
+        kname = "k_conv_lds_pair (" + " + ".join(kernels[v] for v in CONV2) + ")"
+        covers, wl = "one dispatch: conv 2a and 2b paired", "conv 2a + conv 2b (one paired launch)"
+    else:
+        for v, c in CONV2.items():
+            kctx = W.Context(0)
+            try:
+                build_conv(kctx, I, c, "float32", 40, repeat=reps_in_graph)
+                warm[v] = time_ctx(kctx, 20) / reps_in_graph
+            finally:
+                kctx.destroy()
+            n = int(300e6 / conv_bytes(c, 4)) + 1
+            _, _, per_kernel[v] = measure(W, lambda ctx, i, c=c: build_conv(ctx, I, c, "float32", 40 + 10 * i), n,
+                                          reps_shape=5, reps_amort=10)
+        dom = max(per_kernel, key=per_kernel.get)
+        flops_dom, bytes_dom, kname = conv_flops(CONV2[dom]), conv_bytes(CONV2[dom], 4), kernels[dom]
+        covers = ("GEMM dispatch + split-K reduction dispatch" if re.search(r"_k\d+$", kernels[dom])
+                  else "one dispatch")
+        wl = f"conv {dom}"
     dom_ms = per_kernel[dom]
-    achieved = conv_flops(CONV2[dom]) / (dom_ms * 1e-3) / 1e12
-    achieved_warm = conv_flops(CONV2[dom]) / (warm[dom] * 1e-3) / 1e12
+    achieved = flops_dom / (dom_ms * 1e-3) / 1e12
+    achieved_warm = flops_dom / (warm[dom] * 1e-3) / 1e12
     traffic = None if args.no_traffic else measure_traffic(dom)
     roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK["fp32_TFLOPs"],
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK["fp32_TFLOPs"], 4),
                 "traffic": traffic["bytes"] if traffic else None,
-                "kernel": kernels[dom], "workload": f"conv {dom}",
+                "kernel": kname, "workload": wl,
                 "launch_us": round(dom_ms * 1e3, 2),
                 "protocol": "amortised: a graph of instances over >= 300 MB of distinct buffers",
                 "frac_warm": round(achieved_warm / PEAK["fp32_TFLOPs"], 4),
                 "launch_us_warm": round(warm[dom] * 1e3, 2),
-                "launch_covers": ("GEMM dispatch + split-K reduction dispatch"
-                                  if re.search(r"_k\d+$", kernels[dom]) else "one dispatch"),
-                "algorithmic_bytes": conv_bytes(CONV2[dom], 4)}
+                "launch_covers": covers,
+                "algorithmic_bytes": bytes_dom}
     if traffic:
         roofline["traffic_detail"] = traffic
 

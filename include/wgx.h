@@ -283,6 +283,12 @@ int wgx_time_submits(wgx_ctx* ctx, int reps, float* ms_per_submit);
 
 /* Name of the kernel the last wgx_record_* call selected (for tests/profiling). */
 const char* wgx_last_kernel(const wgx_ctx* ctx);
+/* Number of paired launches the last wgx_submit issued: two adjacent
+ * recorded convolutions that read and write disjoint memory and both take
+ * the float32 batch-1 LDS-patch configuration run as one launch (set
+ * WGX_MERGE=0 to keep them apart).  No counterpart in the reference, which
+ * runs every dispatch of a pass on its own; for tests and profiling. */
+int wgx_paired_launches(const wgx_ctx* ctx);
 
 #ifdef __cplusplus
 }

@@ -403,6 +403,65 @@ def test_dense_conv_silu_residual_epilogue(gpu_ctx, orc, pkg, monkeypatch, dtype
                       f"dense residual {i} {dtype} {xs}x{ws} s{s} {kernel}")
 
 
+def test_paired_convolution_launches(gpu_ctx, orc, pkg, monkeypatch):
+    """Two adjacent independent float32 batch-1 convolutions run as one paired
+    launch (both strides, with and without row segments, a bias, SiLU and a
+    residual); a second convolution that reads the first one's output is not
+    paired; WGX_MERGE=0 keeps every launch apart.  Every output against the
+    float64 convolution."""
+    W, I = pkg.wgx, pkg.inputs
+    monkeypatch.delenv("WGX_CONV_LDS", raising=False)
+    shapes = [((1, 32, 20, 24), (48, 32, 3, 3), 1, 1), ((1, 64, 16, 16), (40, 64, 3, 3), 2, 1),
+              ((1, 16, 13, 10), (24, 16, 3, 3), 1, 1), ((1, 24, 21, 19), (16, 24, 3, 3), 2, 0)]
+
+    def record(i, xs, ws, s, p, res=False):
+        x = I.uniform(3400 + i, xs, -1, 1)
+        w = I.uniform(3410 + i, ws, -0.5, 0.5)
+        b = I.uniform(3420 + i, (ws[0],), -0.5, 0.5)
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), 1)
+        tx, tw, tb = gpu_ctx.from_numpy(x, "float32"), gpu_ctx.from_numpy(w, "float32"), gpu_ctx.from_numpy(b, "float32")
+        ty = gpu_ctx.tensor("float32", list(ref.shape))
+        if res:
+            r = I.uniform(3430 + i, ref.shape, -2, 2)
+            tr = gpu_ctx.from_numpy(r, "float32")
+            gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], 1, ty,
+                                activation=W.ACT_SILU, residual=tr, conv_scale=1.0, residual_scale=0.5)
+            want = ref / (1.0 + np.exp(-ref)) + 0.5 * r
+            bound = 1.1 * refa + 0.5 * np.abs(r)
+        else:
+            gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], 1, ty)
+            want, bound = ref, refa
+        assert gpu_ctx.last_kernel.startswith("conv_lds_f32_"), gpu_ctx.last_kernel
+        return ty, want, bound, ws[1] * 9
+
+    for merge, expect in (("1", 2), ("0", 0)):
+        monkeypatch.setenv("WGX_MERGE", merge)
+        gpu_ctx.reset()
+        outs = [record(i, *sh, res=(i == 3)) for i, sh in enumerate(shapes)]
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        assert gpu_ctx.paired_launches == expect
+        for i, (ty, want, bound, K) in enumerate(outs):
+            assert_parity(ty.get_f32(), want, bound, "float32", K, f"paired {merge} conv {i} {shapes[i]}")
+    # b reads a's output: not independent, two launches
+    monkeypatch.setenv("WGX_MERGE", "1")
+    gpu_ctx.reset()
+    x = I.uniform(3500, (1, 16, 12, 12), -1, 1)
+    w1 = I.uniform(3501, (16, 16, 3, 3), -0.5, 0.5)
+    w2 = I.uniform(3502, (8, 16, 3, 3), -0.5, 0.5)
+    tx, t1, t2 = gpu_ctx.from_numpy(x, "float32"), gpu_ctx.from_numpy(w1, "float32"), gpu_ctx.from_numpy(w2, "float32")
+    ty1 = gpu_ctx.tensor("float32", [1, 16, 12, 12])
+    ty2 = gpu_ctx.tensor("float32", [1, 8, 12, 12])
+    gpu_ctx.convolution(tx, t1, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 1, ty1)
+    gpu_ctx.convolution(ty1, t2, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 1, ty2)
+    gpu_ctx.submit()
+    gpu_ctx.sync()
+    assert gpu_ctx.paired_launches == 0
+    y1 = ty1.get_f32()
+    ref2, refa2 = orc.conv2d_f64(y1, w2, None, (1, 1), (1, 1), (1, 1), 1)
+    assert_parity(ty2.get_f32(), ref2, refa2, "float32", 16 * 9, "dependent pair")
+
+
 @pytest.mark.parametrize("dtype", ["float32", "float16"])
 def test_depthwise_silu_residual_epilogue(gpu_ctx, orc, pkg, dtype):
     """Depthwise convolution + SiLU + an output-shaped residual in one launch,

@@ -45,6 +45,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "internal.h"
 
 namespace wgx {
@@ -265,8 +267,10 @@ __device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM
   }
 }
 
+// One tile of the channel-major LDS-patch convolution: block blk of nblk
+// (the launch's whole grid, or one convolution's share of a paired launch).
 template <int DT, int KH, int KW, int S, int TM, int TN, bool RV>
-__global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
+__device__ __forceinline__ void conv_lds_tile(const CParams& p, int blk, int nblk) {
   using G = Geo<DT, KH, KW, S, TN, RV>;
   static_assert(!RV || DT == WGX_FLOAT32, "row segments are 4 float32 pixels");
   constexpr int ES = G::ES, T = G::T, STEPS = G::STEPS, NBLK = G::NBLK, PF = G::PF;
@@ -280,8 +284,8 @@ __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
   // XCD-aware numbering (block ids are dealt round-robin to the 8 XCDs):
   // XCD x gets a contiguous run of tiles; output-channel tiles vary fastest,
   // so the tiles of one pixel region (one input patch) meet in one L2
-  const int Gn = gridDim.x;
-  const int rb = (Gn & 7) == 0 ? (blockIdx.x & 7) * (Gn >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int Gn = nblk;
+  const int rb = (Gn & 7) == 0 ? (blk & 7) * (Gn >> 3) + (blk >> 3) : blk;
   int t = rb;
   const int tm = t % p.tiles_m;
   t /= p.tiles_m;
@@ -499,6 +503,24 @@ __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
 
   conv_epilogue<DT, TM, TN>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
 }
+
+template <int DT, int KH, int KW, int S, int TM, int TN, bool RV>
+__global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
+  conv_lds_tile<DT, KH, KW, S, TM, TN, RV>(p, blockIdx.x, gridDim.x);
+}
+
+// Two independent float32 batch-1 convolutions (32 x 64 tiles, 4 waves per
+// block) in one launch: blocks [0, na) run a's tiles, the rest b's, so the
+// start-up loads of one and the reduction and stores of the other overlap
+// on the same CUs instead of following each other.
+template <int SA, bool RVA, int SB, bool RVB>
+__global__ __launch_bounds__(256) void k_conv_lds_pair(CParams pa, CParams pb, int na) {
+  if ((int)blockIdx.x < na)
+    conv_lds_tile<WGX_FLOAT32, 3, 3, SA, 1, 2, RVA>(pa, blockIdx.x, na);
+  else
+    conv_lds_tile<WGX_FLOAT32, 3, 3, SB, 1, 2, RVB>(pb, blockIdx.x - na, gridDim.x - na);
+}
+
 
 // ------------------------------------------------------------ 16-bit form
 // float16 / bfloat16 with a channel-last patch.  Within a chunk of 16 input
@@ -887,31 +909,8 @@ Cfg choose(const ConvLdsDesc& d, int cus) {
   return c;
 }
 
-}  // namespace
-
-bool conv_lds_applies(const ConvLdsDesc& d) {
-  if (getenv("WGX_CONV_LDS") && strcmp(getenv("WGX_CONV_LDS"), "off") == 0) return false;
-  if (d.dtype != WGX_FLOAT16 && d.dtype != WGX_FLOAT32 && d.dtype != WGX_BFLOAT16) return false;
-  if (d.IC % chunk_channels(d.dtype) != 0 || d.IC <= 0 || d.OC <= 0) return false;
-  const bool geo = (d.KH == 3 && d.KW == 3 && d.sH == d.sW && (d.sH == 1 || d.sH == 2));
-  if (!geo) return false;
-  const int es = d.dtype == WGX_FLOAT32 ? 4 : 2;
-  // 32-bit buffer offsets: one input image and the whole weight tensor
-  if ((long long)d.IC * d.IH * d.IW * es >= (1LL << 31)) return false;
-  if ((long long)d.OC * d.IC * d.KH * d.KW * es >= (1LL << 31)) return false;
-  return true;
-}
-
-hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name) {
-  if (!conv_lds_applies(d)) return hipErrorNotSupported;
-  Cfg c = choose(d, cus);
-  if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
-  // images whose rows are whole 16-byte segments on a 16-byte base (float32:
-  // a multiple of 4 columns, 16-bit: of 8) load the patch as row segments;
-  // WGX_CONV_RV=0 keeps the element loads
-  const bool rv_off = getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0;
-  c.rv = d.IW % (d.dtype == WGX_FLOAT32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
-         (d.dtype == WGX_FLOAT32 || (c.cl && !(c.tm == 2 && c.tn == 1))) && !rv_off;
+// The kernel parameters of d under configuration c.
+CParams make_params(const ConvLdsDesc& d, const Cfg& c) {
   CParams p{};
   p.x = d.x;
   p.w = d.w;
@@ -940,6 +939,64 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   p.res = d.res;
   p.rcs = d.res_conv_scale;
   p.rrs = d.res_scale;
+  return p;
+}
+
+// Images whose rows are whole 16-byte segments on a 16-byte base (float32: a
+// multiple of 4 columns, 16-bit: of 8) load the patch as row segments;
+// WGX_CONV_RV=0 keeps the element loads.
+bool use_rv(const ConvLdsDesc& d, const Cfg& c) {
+  const bool rv_off = getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0;
+  return d.IW % (d.dtype == WGX_FLOAT32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
+         (d.dtype == WGX_FLOAT32 || (c.cl && !(c.tm == 2 && c.tn == 1))) && !rv_off;
+}
+
+template <int SA, bool RVA, int SB, bool RVB>
+hipError_t launch_pair_t(const CParams& pa, const CParams& pb, hipStream_t s) {
+  auto fn = k_conv_lds_pair<SA, RVA, SB, RVB>;
+  const size_t w = (size_t)pa.W;  // both parts run W waves per block
+  const size_t la = w * Geo<WGX_FLOAT32, 3, 3, SA, 2, RVA>::LDS_WAVE;
+  const size_t lb = w * Geo<WGX_FLOAT32, 3, 3, SB, 2, RVB>::LDS_WAVE;
+  const size_t part = w > 1 ? w * 1 * 2 * 4 * 64 * 16 : 0;  // the waves' partial sums
+  const size_t lds = std::max(std::max(la, lb), part);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(fn, dim3((unsigned)(pa.ntiles + pb.ntiles)), dim3(64 * (unsigned)w), lds, s, pa, pb, pa.ntiles);
+  return hipGetLastError();
+}
+
+template <int SA, bool RVA>
+hipError_t launch_pair_b(const CParams& pa, const CParams& pb, int sb, bool rvb, hipStream_t s) {
+  if (sb == 1) return rvb ? launch_pair_t<SA, RVA, 1, true>(pa, pb, s) : launch_pair_t<SA, RVA, 1, false>(pa, pb, s);
+  return rvb ? launch_pair_t<SA, RVA, 2, true>(pa, pb, s) : launch_pair_t<SA, RVA, 2, false>(pa, pb, s);
+}
+
+}  // namespace
+
+bool conv_lds_applies(const ConvLdsDesc& d) {
+  if (getenv("WGX_CONV_LDS") && strcmp(getenv("WGX_CONV_LDS"), "off") == 0) return false;
+  if (d.dtype != WGX_FLOAT16 && d.dtype != WGX_FLOAT32 && d.dtype != WGX_BFLOAT16) return false;
+  if (d.IC % chunk_channels(d.dtype) != 0 || d.IC <= 0 || d.OC <= 0) return false;
+  const bool geo = (d.KH == 3 && d.KW == 3 && d.sH == d.sW && (d.sH == 1 || d.sH == 2));
+  if (!geo) return false;
+  const int es = d.dtype == WGX_FLOAT32 ? 4 : 2;
+  // 32-bit buffer offsets: one input image and the whole weight tensor
+  if ((long long)d.IC * d.IH * d.IW * es >= (1LL << 31)) return false;
+  if ((long long)d.OC * d.IC * d.KH * d.KW * es >= (1LL << 31)) return false;
+  return true;
+}
+
+hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name) {
+  if (!conv_lds_applies(d)) return hipErrorNotSupported;
+  Cfg c = choose(d, cus);
+  if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
+  c.rv = use_rv(d, c);
+  const CParams p = make_params(d, c);
   if (name) {
     char buf[96];
     snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d", c.cl ? "cl" : "lds",
@@ -952,6 +1009,30 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   if (d.dtype == WGX_FLOAT32) return launch_dt<WGX_FLOAT32>(p, c, d.sH, grid, s);
   if (d.dtype == WGX_BFLOAT16) return launch_dt<WGX_BFLOAT16>(p, c, d.sH, grid, s);
   return launch_dt<WGX_FLOAT16>(p, c, d.sH, grid, s);
+}
+
+// Two independent float32 convolutions that both take the batch-1 32 x 64
+// configuration, in one launch of 4-wave blocks (k_conv_lds_pair); the
+// partial sums of a tile are added in the order of its 4 waves.  Not
+// supported (hipErrorNotSupported, nothing launched) for anything else, with
+// a forced configuration (WGX_CONV_LDS) or with WGX_MERGE=0.
+hipError_t launch_conv_lds_pair(const ConvLdsDesc& a, const ConvLdsDesc& b, int cus, hipStream_t s) {
+  const char* m = getenv("WGX_MERGE");
+  if ((m && strcmp(m, "0") == 0) || getenv("WGX_CONV_LDS")) return hipErrorNotSupported;
+  if (a.dtype != WGX_FLOAT32 || b.dtype != WGX_FLOAT32 || !conv_lds_applies(a) || !conv_lds_applies(b))
+    return hipErrorNotSupported;
+  Cfg ca = choose(a, cus), cb = choose(b, cus);
+  if (ca.tm != 1 || ca.tn != 2 || cb.tm != 1 || cb.tn != 2) return hipErrorNotSupported;
+  // 4 waves per block for both (headline step, paired: 32 us at 4 waves,
+  // 40 at 2, 55 at 1; 35.5 us as two launches)
+  ca.w = cb.w = 4;
+  ca.rv = use_rv(a, ca);
+  cb.rv = use_rv(b, cb);
+  const CParams pa = make_params(a, ca), pb = make_params(b, cb);
+  if (pa.ntiles == 0 || pb.ntiles == 0 || (long long)pa.ntiles + pb.ntiles >= (1LL << 31)) return hipErrorNotSupported;
+  if (is_dry(s)) return hipSuccess;
+  if (a.sH == 1) return ca.rv ? launch_pair_b<1, true>(pa, pb, b.sH, cb.rv, s) : launch_pair_b<1, false>(pa, pb, b.sH, cb.rv, s);
+  return ca.rv ? launch_pair_b<2, true>(pa, pb, b.sH, cb.rv, s) : launch_pair_b<2, false>(pa, pb, b.sH, cb.rv, s);
 }
 
 }  // namespace wgx

@@ -110,6 +110,9 @@ struct ConvLdsDesc {
 bool conv_lds_applies(const ConvLdsDesc& d);
 // cus: compute units of the device (the configuration depends on it)
 hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name);
+// Two independent convolutions in one launch where both take the float32
+// batch-1 configuration; hipErrorNotSupported (nothing launched) otherwise.
+hipError_t launch_conv_lds_pair(const ConvLdsDesc& a, const ConvLdsDesc& b, int cus, hipStream_t s);
 
 struct DwDesc {
   int dtype;

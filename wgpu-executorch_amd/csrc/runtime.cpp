@@ -24,6 +24,7 @@
 
 #include <functional>
 #include <map>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -43,11 +44,36 @@ struct Buf {
 // (buffer base, allocation serial) pairs a command reads or writes
 using Uses = std::vector<std::pair<uintptr_t, uint64_t>>;
 
+// An LDS-patch convolution as recorded: what a paired launch needs, and the
+// byte ranges it reads and writes (to tell whether two are independent).
+struct ConvRec {
+  ConvLdsDesc d;
+  int cus;
+  std::vector<std::pair<uintptr_t, uint64_t>> reads;  // (address, bytes)
+  std::pair<uintptr_t, uint64_t> write;
+};
+
 struct Cmd {
   std::function<hipError_t(hipStream_t)> fn;
   std::string name;
   Uses uses;
+  std::shared_ptr<ConvRec> conv;  // set for LDS-patch convolutions
 };
+
+bool ranges_overlap(const std::pair<uintptr_t, uint64_t>& a, const std::pair<uintptr_t, uint64_t>& b) {
+  return a.first < b.first + b.second && b.first < a.first + a.second;
+}
+
+// Two recorded convolutions can run in one launch when neither writes what
+// the other reads or writes.
+bool independent(const ConvRec& a, const ConvRec& b) {
+  if (ranges_overlap(a.write, b.write)) return false;
+  for (const auto& r : b.reads)
+    if (ranges_overlap(a.write, r)) return false;
+  for (const auto& r : a.reads)
+    if (ranges_overlap(b.write, r)) return false;
+  return true;
+}
 
 // What every context on one device shares: the buffer registry and the queue
 // (a single HIP stream), like a GPUDevice and its queue.
@@ -119,6 +145,7 @@ struct wgx_ctx {
   int graph_mode = 1;
   std::string err;
   std::string last_kernel;
+  int paired = 0;  // paired launches the last submit issued
   // the last command, when it is a mergeable max-pool (or a chain of them):
   // stride 1, padding K/2 ("same" size), dilation 1, square odd window
   struct PoolChain {
@@ -326,6 +353,7 @@ int wgx_ctx_has_device(const wgx_ctx* c) { return c && c->d->has_dev ? 1 : 0; }
 const char* wgx_ctx_arch(const wgx_ctx* c) { return c ? c->d->arch.c_str() : ""; }
 void* wgx_ctx_stream(const wgx_ctx* c) { return c ? (void*)c->d->stream : nullptr; }
 const char* wgx_last_kernel(const wgx_ctx* c) { return c ? c->last_kernel.c_str() : ""; }
+int wgx_paired_launches(const wgx_ctx* c) { return c ? c->paired : 0; }
 int wgx_command_count(const wgx_ctx* c) { return c ? (int)c->cmds.size() : 0; }
 
 int wgx_alloc(wgx_ctx* c, uint64_t bytes, uint32_t usage, void** out) {
@@ -729,8 +757,22 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
     if (conv_lds_applies(ld)) {
       const int cus = device_cu_count(c);
       e = launch_conv_lds(ld, cus, c->dry(), &name);
-      if (e == hipSuccess)
-        return c->push([ld, cus](hipStream_t s) { return launch_conv_lds(ld, cus, s, nullptr); }, name);
+      if (e == hipSuccess) {
+        const int pr = c->push([ld, cus](hipStream_t s) { return launch_conv_lds(ld, cus, s, nullptr); }, name);
+        auto rec = std::make_shared<ConvRec>();
+        rec->d = ld;
+        rec->cus = cus;
+        auto range = [](const wgx_tensor* t) {
+          return std::make_pair(reinterpret_cast<uintptr_t>(t->data), (uint64_t)numel(t) * elsize(t->dtype));
+        };
+        rec->reads.push_back(range(in));
+        rec->reads.push_back(range(weight));
+        if (bias) rec->reads.push_back(range(bias));
+        if (res) rec->reads.push_back(range(res));
+        rec->write = range(out);
+        c->cmds.back().conv = rec;
+        return pr;
+      }
       if (e != hipErrorInvalidValue) return c->hip_fail(e, "kernel set-up");
       // a configuration whose LDS does not fit, or a many-tile 16-bit shape
       // that the GEMM kernels below run faster
@@ -1191,13 +1233,30 @@ int wgx_record_softmax(wgx_ctx* c, const wgx_tensor* in, int dim, const wgx_tens
 
 // ------------------------------------------------------------------ execution
 
-static int run_eager(wgx_ctx* c) {
-  for (const Cmd& cmd : c->cmds) {
-    hipError_t e = cmd.fn(c->d->stream);
+// Issues the recorded commands on the context's stream in order; two
+// adjacent independent LDS-patch convolutions that both take the float32
+// batch-1 configuration go out as one paired launch.
+static int issue_all(wgx_ctx* c) {
+  const size_t n = c->cmds.size();
+  c->paired = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const Cmd& cmd = c->cmds[i];
+    if (cmd.conv && i + 1 < n && c->cmds[i + 1].conv && independent(*cmd.conv, *c->cmds[i + 1].conv)) {
+      const hipError_t e = launch_conv_lds_pair(cmd.conv->d, c->cmds[i + 1].conv->d, cmd.conv->cus, c->d->stream);
+      if (e == hipSuccess) {
+        ++c->paired;
+        ++i;
+        continue;
+      }
+      if (e != hipErrorNotSupported) return c->hip_fail(e, cmd.name.c_str());
+    }
+    const hipError_t e = cmd.fn(c->d->stream);
     if (e != hipSuccess) return c->hip_fail(e, cmd.name.c_str());
   }
   return WGX_OK;
 }
+
+static int run_eager(wgx_ctx* c) { return issue_all(c); }
 
 int wgx_submit(wgx_ctx* c) {
   CTX_GUARD(c);
@@ -1208,14 +1267,7 @@ int wgx_submit(wgx_ctx* c) {
   if (!c->graph_valid) {
     hipError_t e = hipStreamBeginCapture(c->d->stream, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) return c->hip_fail(e, "submit: begin capture");
-    int r = WGX_OK;
-    for (const Cmd& cmd : c->cmds) {
-      e = cmd.fn(c->d->stream);
-      if (e != hipSuccess) {
-        r = c->hip_fail(e, cmd.name.c_str());
-        break;
-      }
-    }
+    const int r = issue_all(c);
     hipGraph_t g = nullptr;
     hipError_t e2 = hipStreamEndCapture(c->d->stream, &g);
     if (r != WGX_OK) {

@@ -111,6 +111,7 @@ SIGNATURES = {
     "wgx_set_graph_mode": (_I, [_P, _I]),
     "wgx_time_submits": (_I, [_P, _I, ctypes.POINTER(ctypes.c_float)]),
     "wgx_last_kernel": (ctypes.c_char_p, [_P]),
+    "wgx_paired_launches": (ctypes.c_int, [_P]),
 }
 
 
@@ -219,6 +220,11 @@ class Context:
     @property
     def command_count(self) -> int:
         return lib().wgx_command_count(self.h)
+
+    @property
+    def paired_launches(self) -> int:
+        """Paired convolution launches the last submit issued."""
+        return lib().wgx_paired_launches(self.h)
 
     def destroy(self):
         if not self.destroyed:
