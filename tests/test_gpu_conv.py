@@ -542,8 +542,9 @@ def test_lds_patch_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, form, c
                             clamp=(-0.25, 0.5) if mode == 2 else None,
                             activation=W.ACT_SILU if mode == 1 else W.ACT_NONE)
         kernel = gpu_ctx.last_kernel
+        pre = form == "cl" and cfg == "2x2w1" and s == 1  # pre-ordered weights
         assert kernel.startswith(f"conv_{form}_") and kernel.endswith(
-            f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}"), kernel
+            f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}" + ("_pre" if pre else "")), kernel
         gpu_ctx.submit()
         gpu_ctx.sync()
         got = ty.get_f32()
@@ -601,8 +602,11 @@ def test_channel_last_row_segments(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg, r
         gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], 1, ty,
                             activation=W.ACT_SILU if i % 2 else W.ACT_NONE)
         kernel = gpu_ctx.last_kernel
-        assert kernel.startswith("conv_cl_") and kernel.endswith(
-            f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}"), kernel
+        tile = f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}"
+        # the one-wave 64 x 64 and 64 x 128 tiles at stride 1 run on
+        # pre-ordered weights (a reorder pass first)
+        pre = cfg in ("2x4w1", "2x2w1") and s == 1
+        assert kernel.startswith("conv_cl_") and kernel.endswith(tile + ("_pre" if pre else "")), kernel
         gpu_ctx.submit()
         gpu_ctx.sync()
         if i % 2:
@@ -612,13 +616,18 @@ def test_channel_last_row_segments(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg, r
                       f"cl seg rv={rv} {cfg} case {i} {dtype} {xs}x{ws} s{s} p{p} {kernel}")
 
 
-def test_batched_16bit_convolution_default_choice(gpu_ctx, orc, pkg):
+@pytest.mark.parametrize("pre", ["1", "0"])
+def test_batched_16bit_convolution_default_choice(gpu_ctx, orc, pkg, monkeypatch, pre):
     """Batched 16-bit 3x3 convolutions through the automatic kernel choice:
-    enough tiles for the many-tile rule, which takes the 64 x 128
-    channel-last tile at stride 1; every output element against the float64
+    enough tiles for the many-tile rule, which takes the channel-last kernel
+    at stride 1: the 64 x 64 one-wave tile on pre-ordered weights (a reorder
+    pass into a workspace first) or, with WGX_CONV_PRE=0, the 64 x 128 tile
+    on the raw weights; every output element against the float64
     convolution."""
     I = pkg.inputs
-    cases = [((128, 32, 32, 32), (64, 32, 3, 3), 1, 1, "conv_cl_f16_3x3s1_64x128w1")]
+    monkeypatch.setenv("WGX_CONV_PRE", pre)
+    want = "conv_cl_f16_3x3s1_64x64w1_pre" if pre == "1" else "conv_cl_f16_3x3s1_64x128w1"
+    cases = [((128, 32, 32, 32), (64, 32, 3, 3), 1, 1, want), ((256, 32, 20, 24), (40, 32, 3, 3), 1, 1, want)]
     for i, (xs, ws, s, p, want) in enumerate(cases):
         x = round_in(I.uniform(2900 + i, xs, -1, 1), "float16")
         w = round_in(I.uniform(2910 + i, ws, -0.5, 0.5), "float16")

@@ -566,10 +566,16 @@ struct GeoCL {
 // multiple of 8 columns): a lane loads one segment of each of 8 channels and
 // turns the 8 x 8 block channel-last in registers, 16 bytes per pixel, in
 // place of one 2-byte load per pixel and channel.
-template <int DT, int KH, int KW, int S, int TM, int TN, bool RV>
-__global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p) {
+// PRE: the weights come pre-ordered [OC][chunk][tap][16 channels] (written
+// by k_w_tapmajor), so a fragment is one 16-byte load; they stream RING taps
+// ahead of the multiplies instead of a whole chunk ahead, which frees the
+// registers of the chunk-ahead copy and its rebuild.
+template <int DT, int KH, int KW, int S, int TM, int TN, bool RV, bool PRE = false>
+__global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512)
+__attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl(CParams p) {
   using G = GeoCL<KH, KW, S, TN>;
   constexpr int T = G::T, NBLK = G::NBLK;
+  constexpr int RING = 3;
   constexpr int NL = T;  // 16-byte weight loads per row block per chunk (8 channels x T taps)
   extern __shared__ uint4 lds_u4[];
   char* lds = reinterpret_cast<char*>(lds_u4);
@@ -593,11 +599,13 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
 
   // A: lane offset of its weight row's run (this lane half's 8 channels of
   // the chunk x T taps); rows past OC read zero
+  // (PRE: of its fragment of tap 0 in chunk 0; chunk c, tap t lie (c*T + t)
+  // * 32 bytes further)
   uint32_t va[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int oc = m0 + i * 32 + fr;
-    va[i] = oc < p.OC ? (uint32_t)(oc * K + fc * 8 * T) * 2 : OOB;
+    va[i] = oc < p.OC ? (PRE ? (uint32_t)(oc * K * 2 + fc * 16) : (uint32_t)(oc * K + fc * 8 * T) * 2) : OOB;
   }
   // patch pixel q = e*64 + lane: its input offset in channel 0 of the chunk
   // (OOB outside the image) and its LDS slot (-1 past the patch)
@@ -717,7 +725,14 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
   };
   // the lane's raw weight run of the next chunk (element c*T + t: channel c,
   // tap t) and the fragments of the current one
-  uint4 ra[TM][NL];
+  uint4 ra[PRE ? 1 : TM][PRE ? 1 : NL];
+  // PRE: tap t of chunk c into ring slot t % RING
+  uint4 ar[PRE ? RING : 1][TM];
+  const rsrc_t rwp = rsrc(wbase, wbytes);
+  auto load_tap = [&](int c, int t) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) ar[t % RING][i] = ld16(rwp, va[i], (uint32_t)((c * T + t) * 32));
+  };
   auto load_a = [&](int c) {
     const rsrc_t rw = rsrc(wbase + (long long)c * chunk_w, wbytes - (uint32_t)c * chunk_w);
 #pragma unroll
@@ -725,7 +740,7 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
 #pragma unroll
       for (int s = 0; s < NL; ++s) ra[i][s] = ld16(rw, va[i], (uint32_t)(s * 16));
   };
-  uint4 af[T][TM];
+  uint4 af[PRE ? 1 : T][TM];
   auto build_a = [&]() {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -748,7 +763,12 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
   int c = wave;
   if (c < p.nchunks) {
     load_patch(c);
-    load_a(c);
+    if constexpr (PRE) {
+#pragma unroll
+      for (int t = 0; t < RING; ++t) load_tap(c, t);
+    } else {
+      load_a(c);
+    }
   }
   for (; c < p.nchunks; c += W) {
     const bool more = c + W < p.nchunks;
@@ -756,11 +776,11 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
     // operations run in order), the weights -> fragments, then the next
     // chunk's loads go out behind this chunk's multiplies
     store_patch();
-    build_a();
+    if constexpr (!PRE) build_a();
     asm volatile("" ::: "memory");
     if (more) {
       load_patch(c + W);
-      load_a(c + W);
+      if constexpr (!PRE) load_a(c + W);
     }
     auto read_b = [&](uint4* bf, int t) {
 #pragma unroll
@@ -775,13 +795,32 @@ __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512) void k_conv_cl(CParams p)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) acc[i][j] = mma<DT>(bb[t & 1][j], af[t][i], acc[i][j]);
+        for (int i = 0; i < TM; ++i) acc[i][j] = mma<DT>(bb[t & 1][j], PRE ? ar[t % RING][i] : af[PRE ? 0 : t][i], acc[i][j]);
+      if constexpr (PRE) {
+        // the slot just read takes tap t + RING (of the next chunk past the last tap)
+        if (t + RING < T) load_tap(c, t + RING);
+        else if (more) load_tap(c + W, t + RING - T);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     asm volatile("" ::: "memory");
   }
 
   conv_epilogue<DT, TM, TN>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+}
+
+// 16-bit weights [OC][IC][T] -> [OC][IC/16][T][16]: chunk q's tap t holds
+// its 16 channels in 32 contiguous bytes (the channel-last kernel's PRE form)
+__global__ __launch_bounds__(256) void k_w_tapmajor(const uint16_t* __restrict__ w, uint16_t* __restrict__ wp,
+                                                    long long n, int IC, int T) {
+  const long long per_oc = (long long)IC * T;
+  for (long long d = (long long)blockIdx.x * 256 + threadIdx.x; d < n; d += (long long)gridDim.x * 256) {
+    const long long oc = d / per_oc;
+    const int r = (int)(d - oc * per_oc);
+    const int q = r / (16 * T), r2 = r - q * 16 * T;
+    const int t = r2 / 16, cc = r2 - t * 16;
+    wp[d] = w[(oc * IC + q * 16 + cc) * T + t];
+  }
 }
 
 struct Cfg {
@@ -849,6 +888,31 @@ hipError_t launch_dt(const CParams& p, const Cfg& c, int S, unsigned grid, hipSt
   }
 }
 
+// The channel-last 64 x (32 TN) one-wave tile on pre-ordered weights: the
+// reorder pass into d.wpre, then the kernel reading them.
+template <int DT, bool RV, int TN>
+hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned grid, hipStream_t s) {
+  auto fn = k_conv_cl<DT, 3, 3, 1, 2, TN, RV, true>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const long long n = (long long)p.OC * p.IC * 9;
+  const unsigned rgrid = (unsigned)std::min<long long>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(k_w_tapmajor, dim3(rgrid), dim3(256), 0, s, static_cast<const uint16_t*>(w),
+                     static_cast<uint16_t*>(wpre), n, p.IC, 9);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  CParams q = p;
+  q.w = wpre;
+  const size_t lds = (size_t)GeoCL<3, 3, 1, TN>::LDS_WAVE;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(64), lds, s, q);
+  return hipGetLastError();
+}
+
 // Input channels per chunk: 8 for float32 (the channel-major kernel's lane
 // halves take 4 each), 16 for 16-bit data (8 per lane half, both kernels).
 int chunk_channels(int dtype) { return dtype == WGX_FLOAT32 ? 8 : 16; }
@@ -873,16 +937,21 @@ long long tile_count(const ConvLdsDesc& d, const Cfg& c) {
 Cfg choose(const ConvLdsDesc& d, int cus) {
   const long long simds = 4LL * cus;
   const bool cl = d.dtype != WGX_FLOAT32 && !(getenv("WGX_CONV_CL") && strcmp(getenv("WGX_CONV_CL"), "0") == 0);
-  // many tiles, 16-bit: the 64 x 128 channel-last tile with row-segment patch
-  // loads at stride 1 while it still gives every SIMD a wave ([16,64,80,80]
+  // many tiles, 16-bit: the channel-last kernel with row-segment patch loads
+  // at stride 1 while a 64 x 128 tiling still gives every SIMD a wave ([16,64,80,80]
   // -> 128: 60.9 us, [64,64,80,80]: 199 us, [8,32,160,160] -> 64: 45.9 us,
   // against 68.9 / 222 / 64.5 us for the LDS-staged GEMM); otherwise the GEMM
   // ([16,128,40,40] -> 256: 46.7 us against 56.8 for 32 x 64 one-wave tiles)
+  // With pre-ordered weights (WGX_CONV_PRE, default on) the 64 x 64 tile
+  // fits three waves per SIMD and wins: [64,64,80,80] 198 against 213 us for
+  // 64 x 128, [8,32,160,160] 39.1 against 50.0 us.
   auto many16 = [&]() {
     const bool seg = cl && d.IW % 8 == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
                      !(getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0);
+    const bool pre = !(getenv("WGX_CONV_PRE") && strcmp(getenv("WGX_CONV_PRE"), "0") == 0);
     Cfg m{2, 4, 1, cl};
     if (!(seg && d.sH == 1 && tile_count(d, m) >= simds)) m.tm = 0;
+    else if (pre) m.tn = 2;
     return m;
   };
   Cfg c{2, 2, 1, cl};
@@ -991,21 +1060,47 @@ bool conv_lds_applies(const ConvLdsDesc& d) {
   return true;
 }
 
+// The channel-last one-wave 64 x 64 and 64 x 128 tiles at stride 1 (the
+// batched 16-bit choice) run on weights pre-ordered by a small pass into a
+// workspace of OC * IC * 9 elements (WGX_CONV_PRE=0: on the raw weights).
+bool conv_lds_wants_prepass(const ConvLdsDesc& d, int cus) {
+  if (getenv("WGX_CONV_PRE") && strcmp(getenv("WGX_CONV_PRE"), "0") == 0) return false;
+  if (!conv_lds_applies(d) || d.dtype == WGX_FLOAT32 || d.KH != 3 || d.KW != 3 || d.sH != 1) return false;
+  const Cfg c = choose(d, cus);
+  return c.cl && c.tm == 2 && (c.tn == 4 || c.tn == 2) && c.w == 1;
+}
+
 hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name) {
   if (!conv_lds_applies(d)) return hipErrorNotSupported;
   Cfg c = choose(d, cus);
   if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
   c.rv = use_rv(d, c);
   const CParams p = make_params(d, c);
+  const bool pre = d.wpre && c.cl && c.tm == 2 && (c.tn == 4 || c.tn == 2) && c.w == 1 && d.sH == 1;
   if (name) {
     char buf[96];
-    snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d", c.cl ? "cl" : "lds",
+    snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d%s", c.cl ? "cl" : "lds",
              d.dtype == WGX_FLOAT32 ? "f32" : (d.dtype == WGX_BFLOAT16 ? "bf16" : "f16"), d.KH, d.KW, d.sH,
-             32 * c.tm, 32 * c.tn, c.w);
+             32 * c.tm, 32 * c.tn, c.w, pre ? "_pre" : "");
     *name = buf;
   }
   if (p.ntiles == 0) return hipSuccess;
   const unsigned grid = (unsigned)p.ntiles;
+  if (pre) {
+    if (is_dry(s)) return hipSuccess;
+    if (c.tn == 2) {
+      if (d.dtype == WGX_BFLOAT16)
+        return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 2>(p, d.w, d.wpre, grid, s)
+                    : launch_cl_pre<WGX_BFLOAT16, false, 2>(p, d.w, d.wpre, grid, s);
+      return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 2>(p, d.w, d.wpre, grid, s)
+                  : launch_cl_pre<WGX_FLOAT16, false, 2>(p, d.w, d.wpre, grid, s);
+    }
+    if (d.dtype == WGX_BFLOAT16)
+      return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 4>(p, d.w, d.wpre, grid, s)
+                  : launch_cl_pre<WGX_BFLOAT16, false, 4>(p, d.w, d.wpre, grid, s);
+    return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 4>(p, d.w, d.wpre, grid, s)
+                : launch_cl_pre<WGX_FLOAT16, false, 4>(p, d.w, d.wpre, grid, s);
+  }
   if (d.dtype == WGX_FLOAT32) return launch_dt<WGX_FLOAT32>(p, c, d.sH, grid, s);
   if (d.dtype == WGX_BFLOAT16) return launch_dt<WGX_BFLOAT16>(p, c, d.sH, grid, s);
   return launch_dt<WGX_FLOAT16>(p, c, d.sH, grid, s);

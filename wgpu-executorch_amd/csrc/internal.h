@@ -106,8 +106,12 @@ struct ConvLdsDesc {
   // y = res_conv_scale * y + res_scale * res (null: none)
   const void* res;
   float res_conv_scale, res_scale;
+  // workspace for the pre-ordered weights (OC * IC * KH * KW elements) when
+  // conv_lds_wants_prepass says the configuration uses them, else null
+  void* wpre;
 };
 bool conv_lds_applies(const ConvLdsDesc& d);
+bool conv_lds_wants_prepass(const ConvLdsDesc& d, int cus);
 // cus: compute units of the device (the configuration depends on it)
 hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name);
 // Two independent convolutions in one launch where both take the float32

@@ -756,6 +756,10 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
     ld.res_scale = rrs;
     if (conv_lds_applies(ld)) {
       const int cus = device_cu_count(c);
+      if (conv_lds_wants_prepass(ld, cus)) {
+        ld.wpre = c->owned_alloc((uint64_t)numel(weight) * elsize(weight->dtype));
+        if (!ld.wpre) return c->fail(WGX_ERR_OOM, "convolution: pre-ordered weight workspace allocation failed");
+      }
       e = launch_conv_lds(ld, cus, c->dry(), &name);
       if (e == hipSuccess) {
         const int pr = c->push([ld, cus](hipStream_t s) { return launch_conv_lds(ld, cus, s, nullptr); }, name);
