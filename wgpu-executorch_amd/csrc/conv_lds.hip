@@ -566,8 +566,9 @@ struct GeoCL {
 // multiple of 8 columns): a lane loads one segment of each of 8 channels and
 // turns the 8 x 8 block channel-last in registers, 16 bytes per pixel, in
 // place of one 2-byte load per pixel and channel.
-// PRE: the weights come pre-ordered [OC][chunk][tap][16 channels] (written
-// by k_w_tapmajor), so a fragment is one 16-byte load; they stream RING taps
+// PRE: the weights come pre-ordered [chunk][tap][OC][16 channels] (written
+// by k_w_tapmajor), so a fragment is one 16-byte load and a row block's 32
+// rows are contiguous; they stream RING taps
 // ahead of the multiplies instead of a whole chunk ahead, which frees the
 // registers of the chunk-ahead copy and its rebuild.
 template <int DT, int KH, int KW, int S, int TM, int TN, bool RV, bool PRE = false>
@@ -600,12 +601,12 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   // A: lane offset of its weight row's run (this lane half's 8 channels of
   // the chunk x T taps); rows past OC read zero
   // (PRE: of its fragment of tap 0 in chunk 0; chunk c, tap t lie (c*T + t)
-  // * 32 bytes further)
+  // * OC * 32 bytes further)
   uint32_t va[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int oc = m0 + i * 32 + fr;
-    va[i] = oc < p.OC ? (PRE ? (uint32_t)(oc * K * 2 + fc * 16) : (uint32_t)(oc * K + fc * 8 * T) * 2) : OOB;
+    va[i] = oc < p.OC ? (PRE ? (uint32_t)(oc * 32 + fc * 16) : (uint32_t)(oc * K + fc * 8 * T) * 2) : OOB;
   }
   // patch pixel q = e*64 + lane: its input offset in channel 0 of the chunk
   // (OOB outside the image) and its LDS slot (-1 past the patch)
@@ -731,7 +732,7 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   const rsrc_t rwp = rsrc(wbase, wbytes);
   auto load_tap = [&](int c, int t) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) ar[t % RING][i] = ld16(rwp, va[i], (uint32_t)((c * T + t) * 32));
+    for (int i = 0; i < TM; ++i) ar[t % RING][i] = ld16(rwp, va[i], (uint32_t)((c * T + t) * p.OC * 32));
   };
   auto load_a = [&](int c) {
     const rsrc_t rw = rsrc(wbase + (long long)c * chunk_w, wbytes - (uint32_t)c * chunk_w);
@@ -809,17 +810,19 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   conv_epilogue<DT, TM, TN>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
 }
 
-// 16-bit weights [OC][IC][T] -> [OC][IC/16][T][16]: chunk q's tap t holds
-// its 16 channels in 32 contiguous bytes (the channel-last kernel's PRE form)
+// 16-bit weights [OC][IC][T] -> [IC/16][T][OC][16]: for chunk q and tap t
+// the 16 channels of consecutive output channels are consecutive 32-byte
+// pieces, so the 32 rows of a weight fragment load are 1 KB of contiguous
+// memory (the channel-last kernel's PRE form)
 __global__ __launch_bounds__(256) void k_w_tapmajor(const uint16_t* __restrict__ w, uint16_t* __restrict__ wp,
-                                                    long long n, int IC, int T) {
-  const long long per_oc = (long long)IC * T;
+                                                    long long n, int OC, int IC, int T) {
   for (long long d = (long long)blockIdx.x * 256 + threadIdx.x; d < n; d += (long long)gridDim.x * 256) {
-    const long long oc = d / per_oc;
-    const int r = (int)(d - oc * per_oc);
-    const int q = r / (16 * T), r2 = r - q * 16 * T;
-    const int t = r2 / 16, cc = r2 - t * 16;
-    wp[d] = w[(oc * IC + q * 16 + cc) * T + t];
+    const int cc = (int)(d & 15);
+    const long long rest = d >> 4;
+    const int oc = (int)(rest % OC);
+    const long long qt = rest / OC;
+    const int t = (int)(qt % T), q = (int)(qt / T);
+    wp[d] = w[((long long)oc * IC + q * 16 + cc) * T + t];
   }
 }
 
@@ -903,7 +906,7 @@ hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned g
   const long long n = (long long)p.OC * p.IC * 9;
   const unsigned rgrid = (unsigned)std::min<long long>((n + 255) / 256, 1024);
   hipLaunchKernelGGL(k_w_tapmajor, dim3(rgrid), dim3(256), 0, s, static_cast<const uint16_t*>(w),
-                     static_cast<uint16_t*>(wpre), n, p.IC, 9);
+                     static_cast<uint16_t*>(wpre), n, p.OC, p.IC, 9);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   CParams q = p;
