@@ -125,8 +125,9 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     # dense 3x3 over a multiple of 16 channels: the LDS-patch kernel at batch
     # 1 (32 x 64 tiles, 64 x 32 for 16-bit data at stride 2, W waves up to
     # the 16-channel chunk count), 64 x 64 one-wave tiles for batched float32,
-    # for batched 16-bit data at stride 1 the 64 x 128 channel-last tile while
-    # it gives every SIMD a wave, else the GEMM kernels
+    # for batched 16-bit data the 64 x 64 channel-last tile on pre-ordered
+    # weights while it gives every SIMD a wave (WGX_CONV_PRE=0: the 64 x 128
+    # tile at stride 1), else the GEMM kernels
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_32x64w4"
     assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1)) == "conv_cl_f16_3x3s2_64x32w8"
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="float32") == "conv_lds_f32_3x3s1_32x64w4"
@@ -136,8 +137,21 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1_pre"
     assert conv([64, 64, 80, 80], [128, 64, 3, 3], [64, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1_pre"
     assert conv([8, 32, 160, 160], [64, 32, 3, 3], [8, 64, 160, 160], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1_pre"
+    assert conv([16, 128, 40, 40], [256, 128, 3, 3], [16, 256, 40, 40], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1_pre"
+    assert conv([64, 128, 80, 80], [256, 128, 3, 3], [64, 256, 40, 40], (2, 2), (1, 1)) == "conv_cl_f16_3x3s2_64x64w1_pre"
+    assert conv([2, 128, 40, 40], [256, 128, 3, 3], [2, 256, 40, 40], pad=(1, 1)) == "conv_cl_f16_3x3s1_32x64w8"
+    # bfloat16 has no im2col GEMM: 1x1 convolutions take the plain GEMM, other
+    # spatial kernels outside the LDS-patch kernel the direct one, and the
+    # many-tile rule keeps the 64 x 64 LDS-patch tile
+    assert conv([1, 8, 20, 20], [16, 8, 5, 5], [1, 16, 16, 16], dtype="bfloat16") == "conv_grouped_direct"
+    assert conv([1, 32, 40, 40], [64, 32, 1, 1], [1, 64, 40, 40], dtype="bfloat16").startswith("gemm_mfma_bf16_")
+    assert conv([64, 32, 40, 41], [64, 32, 3, 3], [64, 64, 40, 41], pad=(1, 1), dtype="bfloat16") == "conv_cl_bf16_3x3s1_64x64w1_pre"
+    monkeypatch.setenv("WGX_CONV_PRE", "0")
+    assert conv([64, 128, 80, 80], [256, 128, 3, 3], [64, 256, 40, 40], (2, 2), (1, 1), dtype="bfloat16") == "conv_cl_bf16_3x3s2_64x64w1"
+    assert conv([64, 64, 80, 80], [128, 64, 3, 3], [64, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x128w1"
     assert conv([16, 128, 40, 40], [256, 128, 3, 3], [16, 256, 40, 40], pad=(1, 1)).startswith("gemm_mfma_f16")
     assert conv([64, 128, 80, 80], [256, 128, 3, 3], [64, 256, 40, 40], (2, 2), (1, 1)).startswith("gemm_mfma_f16")
+    monkeypatch.delenv("WGX_CONV_PRE")
     assert conv([4, 64, 80, 80], [128, 64, 3, 3], [4, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_32x64w2"
     monkeypatch.setenv("WGX_CONV_LDS", "2x1w2")
     assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x32w2"

@@ -542,7 +542,7 @@ def test_lds_patch_configurations(gpu_ctx, orc, pkg, monkeypatch, dtype, form, c
                             clamp=(-0.25, 0.5) if mode == 2 else None,
                             activation=W.ACT_SILU if mode == 1 else W.ACT_NONE)
         kernel = gpu_ctx.last_kernel
-        pre = form == "cl" and cfg == "2x2w1" and s == 1  # pre-ordered weights
+        pre = form == "cl" and cfg == "2x2w1"  # pre-ordered weights
         assert kernel.startswith(f"conv_{form}_") and kernel.endswith(
             f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}" + ("_pre" if pre else "")), kernel
         gpu_ctx.submit()
@@ -603,9 +603,9 @@ def test_channel_last_row_segments(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg, r
                             activation=W.ACT_SILU if i % 2 else W.ACT_NONE)
         kernel = gpu_ctx.last_kernel
         tile = f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}"
-        # the one-wave 64 x 64 and 64 x 128 tiles at stride 1 run on
-        # pre-ordered weights (a reorder pass first)
-        pre = cfg in ("2x4w1", "2x2w1") and s == 1
+        # the one-wave 64 x 64 tile (either stride) and 64 x 128 tile (stride
+        # 1) run on pre-ordered weights (a reorder pass first)
+        pre = cfg in ("2x4w1", "2x2w1")
         assert kernel.startswith("conv_cl_") and kernel.endswith(tile + ("_pre" if pre else "")), kernel
         gpu_ctx.submit()
         gpu_ctx.sync()
@@ -619,22 +619,24 @@ def test_channel_last_row_segments(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg, r
 @pytest.mark.parametrize("pre", ["1", "0"])
 def test_batched_16bit_convolution_default_choice(gpu_ctx, orc, pkg, monkeypatch, pre):
     """Batched 16-bit 3x3 convolutions through the automatic kernel choice:
-    enough tiles for the many-tile rule, which takes the channel-last kernel
-    at stride 1: the 64 x 64 one-wave tile on pre-ordered weights (a reorder
-    pass into a workspace first) or, with WGX_CONV_PRE=0, the 64 x 128 tile
-    on the raw weights; every output element against the float64
-    convolution."""
+    enough tiles for the many-tile rule, which takes the channel-last kernel:
+    the 64 x 64 one-wave tile on pre-ordered weights (a reorder pass into a
+    workspace first) at either stride or, with WGX_CONV_PRE=0, the 64 x 128
+    tile on the raw weights at stride 1 and the GEMM at stride 2; every
+    output element against the float64 convolution."""
     I = pkg.inputs
     monkeypatch.setenv("WGX_CONV_PRE", pre)
     want = "conv_cl_f16_3x3s1_64x64w1_pre" if pre == "1" else "conv_cl_f16_3x3s1_64x128w1"
-    cases = [((128, 32, 32, 32), (64, 32, 3, 3), 1, 1, want), ((256, 32, 20, 24), (40, 32, 3, 3), 1, 1, want)]
+    want2 = "conv_cl_f16_3x3s2_64x64w1_pre" if pre == "1" else "gemm_mfma_f16"
+    cases = [((128, 32, 32, 32), (64, 32, 3, 3), 1, 1, want), ((256, 32, 20, 24), (40, 32, 3, 3), 1, 1, want),
+             ((512, 32, 20, 24), (40, 32, 3, 3), 2, 1, want2)]
     for i, (xs, ws, s, p, want) in enumerate(cases):
         x = round_in(I.uniform(2900 + i, xs, -1, 1), "float16")
         w = round_in(I.uniform(2910 + i, ws, -0.5, 0.5), "float16")
         b = round_in(I.uniform(2920 + i, (ws[0],), -0.5, 0.5), "float16")
         ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), 1)
         got, kernel = run_conv(gpu_ctx, x, w, b, "float16", (s, s), (p, p), out_shape=list(ref.shape))
-        assert kernel == want, kernel
+        assert kernel.startswith(want), kernel
         assert_parity(got, ref, refa, "float16", ws[1] * 9, f"batched {i} {xs}x{ws} s{s} {kernel}")
 
 
@@ -668,3 +670,35 @@ def test_lds_patch_float32_eight_channel_chunks(gpu_ctx, orc, pkg, monkeypatch, 
             ref = ref / (1.0 + np.exp(-ref))
             refa = 1.1 * refa
         assert_parity(ty.get_f32(), ref, refa, "float32", ws[1] * 9, f"lds f32 {cfg} case {i} {xs}x{ws} s{s} {kernel}")
+
+
+# bfloat16 dense convolutions on every route (the GEMM's im2col mode is built
+# for float32 and float16 only): the direct kernel for spatial kernels the
+# LDS-patch kernel does not take, the plain GEMM for 1x1 convolutions with
+# few tiles, and the 64 x 64 LDS-patch tile where float16 would take the
+# GEMM (widths not a multiple of 8, stride 2 without pre-ordered weights)
+BF16_ROUTE_CASES = [
+    ((1, 8, 20, 20), (16, 8, 5, 5), 1, 2, {}, "conv_grouped_direct"),
+    ((2, 24, 20, 20), (16, 24, 3, 3), 1, 1, {}, "conv_grouped_direct"),
+    ((1, 32, 40, 40), (64, 32, 1, 1), 1, 0, {}, "gemm_mfma_bf16_"),
+    ((2, 48, 12, 12), (24, 48, 1, 1), 2, 0, {}, "conv_grouped_direct"),
+    ((64, 32, 40, 41), (64, 32, 3, 3), 1, 1, {}, "conv_cl_bf16_3x3s1_64x64w1_pre"),
+    ((512, 32, 20, 24), (40, 32, 3, 3), 2, 1, {"WGX_CONV_PRE": "0"}, "conv_cl_bf16_3x3s2_64x64w1"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(BF16_ROUTE_CASES)))
+def test_bfloat16_convolution_routes(gpu_ctx, orc, pkg, monkeypatch, case):
+    """Each bfloat16 route records (no set-up failure), names the expected
+    kernel and matches the float64 convolution on every element."""
+    I = pkg.inputs
+    xs, ws, s, p, env, want = BF16_ROUTE_CASES[case]
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    x = round_in(I.uniform(3900 + case, xs, -1, 1), "bfloat16")
+    w = round_in(I.uniform(3910 + case, ws, -0.5, 0.5), "bfloat16")
+    b = round_in(I.uniform(3920 + case, (ws[0],), -0.5, 0.5), "bfloat16")
+    ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), 1)
+    got, kernel = run_conv(gpu_ctx, x, w, b, "bfloat16", (s, s), (p, p), out_shape=list(ref.shape))
+    assert kernel.startswith(want), kernel
+    assert_parity(got, ref, refa, "bfloat16", ws[1] * ws[2] * ws[3], f"bf16 route {case} {xs}x{ws} s{s} {kernel}")

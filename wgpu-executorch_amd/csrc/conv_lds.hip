@@ -893,9 +893,9 @@ hipError_t launch_dt(const CParams& p, const Cfg& c, int S, unsigned grid, hipSt
 
 // The channel-last 64 x (32 TN) one-wave tile on pre-ordered weights: the
 // reorder pass into d.wpre, then the kernel reading them.
-template <int DT, bool RV, int TN>
+template <int DT, bool RV, int TN, int S>
 hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned grid, hipStream_t s) {
-  auto fn = k_conv_cl<DT, 3, 3, 1, 2, TN, RV, true>;
+  auto fn = k_conv_cl<DT, 3, 3, S, 2, TN, RV, true>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -911,7 +911,7 @@ hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned g
   if (e != hipSuccess) return e;
   CParams q = p;
   q.w = wpre;
-  const size_t lds = (size_t)GeoCL<3, 3, 1, TN>::LDS_WAVE;
+  const size_t lds = (size_t)GeoCL<3, 3, S, TN>::LDS_WAVE;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(64), lds, s, q);
   return hipGetLastError();
 }
@@ -946,15 +946,26 @@ Cfg choose(const ConvLdsDesc& d, int cus) {
   // against 68.9 / 222 / 64.5 us for the LDS-staged GEMM); otherwise the GEMM
   // ([16,128,40,40] -> 256: 46.7 us against 56.8 for 32 x 64 one-wave tiles)
   // With pre-ordered weights (WGX_CONV_PRE, default on) the 64 x 64 tile
-  // fits three waves per SIMD and wins: [64,64,80,80] 198 against 213 us for
-  // 64 x 128, [8,32,160,160] 39.1 against 50.0 us.
+  // fits three waves per SIMD and wins at both strides while it gives every
+  // SIMD a wave: [64,64,80,80] 151 us (64 x 128: 213), [8,32,160,160] 39.1
+  // (50.0), [16,128,40,40] -> 256 37.7 (GEMM 47.1), stride 2
+  // [64,128,80,80] -> 256 181 (GEMM 211), [16,128,80,80] 52.4 (57.8).
+  // bfloat16 has no im2col GEMM and keeps the 64 x 64 tile where float16
+  // would take the GEMM.
   auto many16 = [&]() {
     const bool seg = cl && d.IW % 8 == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
                      !(getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0);
     const bool pre = !(getenv("WGX_CONV_PRE") && strcmp(getenv("WGX_CONV_PRE"), "0") == 0);
     Cfg m{2, 4, 1, cl};
-    if (!(seg && d.sH == 1 && tile_count(d, m) >= simds)) m.tm = 0;
-    else if (pre) m.tn = 2;
+    if (pre) {
+      // the 64 x 64 tile, at either stride, while it gives every SIMD a wave
+      m.tn = 2;
+      if (!(seg && tile_count(d, m) >= simds)) m.tm = 0;
+    } else if (!(seg && d.sH == 1 && tile_count(d, m) >= simds)) {
+      m.tm = 0;
+    }
+    // no bfloat16 im2col GEMM: the 64 x 64 one-wave tile
+    if (m.tm == 0 && d.dtype == WGX_BFLOAT16) m = Cfg{2, 2, 1, cl};
     return m;
   };
   Cfg c{2, 2, 1, cl};
@@ -1063,14 +1074,15 @@ bool conv_lds_applies(const ConvLdsDesc& d) {
   return true;
 }
 
-// The channel-last one-wave 64 x 64 and 64 x 128 tiles at stride 1 (the
-// batched 16-bit choice) run on weights pre-ordered by a small pass into a
-// workspace of OC * IC * 9 elements (WGX_CONV_PRE=0: on the raw weights).
+// The channel-last one-wave 64 x 64 tile (either stride) and 64 x 128 tile
+// (stride 1) -- the batched 16-bit choice -- run on weights pre-ordered by a
+// small pass into a workspace of OC * IC * 9 elements (WGX_CONV_PRE=0: on
+// the raw weights).
 bool conv_lds_wants_prepass(const ConvLdsDesc& d, int cus) {
   if (getenv("WGX_CONV_PRE") && strcmp(getenv("WGX_CONV_PRE"), "0") == 0) return false;
-  if (!conv_lds_applies(d) || d.dtype == WGX_FLOAT32 || d.KH != 3 || d.KW != 3 || d.sH != 1) return false;
+  if (!conv_lds_applies(d) || d.dtype == WGX_FLOAT32 || d.KH != 3 || d.KW != 3) return false;
   const Cfg c = choose(d, cus);
-  return c.cl && c.tm == 2 && (c.tn == 4 || c.tn == 2) && c.w == 1;
+  return c.cl && c.tm == 2 && c.w == 1 && (c.tn == 2 || (c.tn == 4 && d.sH == 1));
 }
 
 hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name) {
@@ -1079,7 +1091,7 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
   c.rv = use_rv(d, c);
   const CParams p = make_params(d, c);
-  const bool pre = d.wpre && c.cl && c.tm == 2 && (c.tn == 4 || c.tn == 2) && c.w == 1 && d.sH == 1;
+  const bool pre = d.wpre && c.cl && c.tm == 2 && c.w == 1 && (c.tn == 2 || (c.tn == 4 && d.sH == 1));
   if (name) {
     char buf[96];
     snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d%s", c.cl ? "cl" : "lds",
@@ -1091,18 +1103,26 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   const unsigned grid = (unsigned)p.ntiles;
   if (pre) {
     if (is_dry(s)) return hipSuccess;
-    if (c.tn == 2) {
-      if (d.dtype == WGX_BFLOAT16)
-        return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 2>(p, d.w, d.wpre, grid, s)
-                    : launch_cl_pre<WGX_BFLOAT16, false, 2>(p, d.w, d.wpre, grid, s);
-      return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 2>(p, d.w, d.wpre, grid, s)
-                  : launch_cl_pre<WGX_FLOAT16, false, 2>(p, d.w, d.wpre, grid, s);
+    const bool bf = d.dtype == WGX_BFLOAT16;
+    if (c.tn == 2 && d.sH == 2) {
+      if (bf)
+        return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 2, 2>(p, d.w, d.wpre, grid, s)
+                    : launch_cl_pre<WGX_BFLOAT16, false, 2, 2>(p, d.w, d.wpre, grid, s);
+      return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 2, 2>(p, d.w, d.wpre, grid, s)
+                  : launch_cl_pre<WGX_FLOAT16, false, 2, 2>(p, d.w, d.wpre, grid, s);
     }
-    if (d.dtype == WGX_BFLOAT16)
-      return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 4>(p, d.w, d.wpre, grid, s)
-                  : launch_cl_pre<WGX_BFLOAT16, false, 4>(p, d.w, d.wpre, grid, s);
-    return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 4>(p, d.w, d.wpre, grid, s)
-                : launch_cl_pre<WGX_FLOAT16, false, 4>(p, d.w, d.wpre, grid, s);
+    if (c.tn == 2) {
+      if (bf)
+        return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 2, 1>(p, d.w, d.wpre, grid, s)
+                    : launch_cl_pre<WGX_BFLOAT16, false, 2, 1>(p, d.w, d.wpre, grid, s);
+      return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 2, 1>(p, d.w, d.wpre, grid, s)
+                  : launch_cl_pre<WGX_FLOAT16, false, 2, 1>(p, d.w, d.wpre, grid, s);
+    }
+    if (bf)
+      return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 4, 1>(p, d.w, d.wpre, grid, s)
+                  : launch_cl_pre<WGX_BFLOAT16, false, 4, 1>(p, d.w, d.wpre, grid, s);
+    return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 4, 1>(p, d.w, d.wpre, grid, s)
+                : launch_cl_pre<WGX_FLOAT16, false, 4, 1>(p, d.w, d.wpre, grid, s);
   }
   if (d.dtype == WGX_FLOAT32) return launch_dt<WGX_FLOAT32>(p, c, d.sH, grid, s);
   if (d.dtype == WGX_BFLOAT16) return launch_dt<WGX_BFLOAT16>(p, c, d.sH, grid, s);

@@ -778,7 +778,7 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
         return pr;
       }
       if (e != hipErrorInvalidValue) return c->hip_fail(e, "kernel set-up");
-      // a configuration whose LDS does not fit, or a many-tile 16-bit shape
+      // a configuration whose LDS does not fit, or a many-tile float16 shape
       // that the GEMM kernels below run faster
     }
   }
@@ -793,9 +793,12 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
   // which splits K over the waves of each tile (measured on the YOLO-N 640
   // frame, whose 1x1 convolutions at 80x80 and below have 28-200 tiles:
   // 527 -> 481 us).
+  // The GEMM's im2col mode is built for float32 and float16 only: a bfloat16
+  // 1x1 convolution always takes the plain [IC, H*W] form, other bfloat16
+  // convolutions that the LDS-patch kernel does not take the direct kernel.
   const long long pw_tiles = (OC + 63) / 64 * ((OH * OW + 63) / 64) * B;
   const bool pointwise = KH == 1 && KW == 1 && sH == 1 && sW == 1 && pH == 0 && pW == 0 &&
-                         pw_tiles >= device_cu_count(c);
+                         (pw_tiles >= device_cu_count(c) || dt == WGX_BFLOAT16);
   // a few taps per output channel in a spatial kernel (network stems, K =
   // IC*KH*KW <= 32, KH*KW > 1): the direct small-tap kernel, not a GEMM with a
   // 1-2 step K loop ([1,3,640,640]*[16,3,3,3] s2: 14.7 against 28.4 us).  A
@@ -806,7 +809,7 @@ static int record_conv(wgx_ctx* c, const wgx_tensor* in, const wgx_tensor* weigh
   const bool small_taps = !args->transposed && groups == 1 && !pointwise && KH * KW > 1 && IC * KH * KW <= 32 &&
                           OC <= 64 && !(st_env && strcmp(st_env, "0") == 0);
   const bool gemm_ok = !args->transposed && groups == 1 && !small_taps &&
-                       (pointwise || conv_ktab_fits((int)(IC * KH * KW), (int)IC, geom));
+                       (pointwise || (dt != WGX_BFLOAT16 && conv_ktab_fits((int)(IC * KH * KW), (int)IC, geom)));
   if (gemm_ok) {
     GemmDesc d{};
     d.dtype = dt;
