@@ -171,9 +171,11 @@ struct Geo {
 // 4*(lane / 32) + e.  With W > 1 waves per block the partial sums of the
 // block's waves meet in LDS and are added in wave order, then bias,
 // activation and clamp, one rounding, 8- or 16-byte stores.
-template <int DT, int TM, int TN>
-__device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM][TN], char* lds, int W, int wave,
-                                              int lane, int m0, int oh0, int ow0, int z, const float (&brow)[TM]) {
+// CL / RS: the launch clamps / adds a residual (one instantiation each, so
+// the per-element code carries no selects for what the launch does not do).
+template <int DT, int TM, int TN, bool CL, bool RS>
+__device__ __forceinline__ void conv_epilogue_t(const CParams& p, f32x16 (&acc)[TM][TN], char* lds, int W, int wave,
+                                                int lane, int m0, int oh0, int ow0, int z, const float (&brow)[TM]) {
   constexpr int ES = DT == WGX_FLOAT32 ? 4 : 2;
   constexpr int NG = TM * TN * 4;
   const int fr = lane & 31, fc = lane >> 5;
@@ -190,8 +192,98 @@ __device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM
               make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
     __syncthreads();
   }
-  const bool vec = (p.OW & 3) == 0;
   char* yimg = static_cast<char*>(p.y) + (long long)z * p.sy * ES;
+  if constexpr (ES == 2) {
+    // 16-bit: lane (fr, fc) holds columns 4fc..4fc+3 of rows 2gp and 2gp+1
+    // of output channel fr; v_permlane32_swap trades the upper half-wave's
+    // row 2gp for the lower half-wave's row 2gp+1, so lane fr then holds all
+    // 8 columns of row 2gp and lane fr + 32 all 8 of row 2gp + 1, and each
+    // lane writes one 16-byte run (half the store instructions, and half the
+    // separate runs the address unit takes, of 8-byte pieces)
+    const bool vec8 = (p.OW & 7) == 0 && ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 15) == 0;
+    const bool vec4 = (p.OW & 3) == 0;
+    auto store_rows = [&](int i, int j, int gp, const float4& a, const float4& b) {
+      const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+      float v[8];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(av[d]), __float_as_uint(bv[d]), false, false);
+        v[d] = __uint_as_float(r[0]);
+        v[4 + d] = __uint_as_float(r[1]);
+      }
+      const int oc = m0 + i * 32 + fr, oh = oh0 + 4 * j + 2 * gp + fc;
+      if (oc >= p.OC || oh >= p.OH || ow0 >= p.OW) return;
+      float bias = 0.0f;
+#pragma unroll
+      for (int ii = 0; ii < TM; ++ii)
+        if (ii == i) bias = brow[ii];
+      const long long eo = (long long)oc * p.OH * p.OW + (long long)oh * p.OW + ow0;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(yimg) + eo;
+      const bool full = ow0 + 7 < p.OW;
+      // the residual's elements at the output's positions, read by the lane
+      // that writes them (a residual that is the output itself is fine)
+      uint32_t rr[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+      if constexpr (RS) {
+        const uint16_t* rp = static_cast<const uint16_t*>(p.res) + (long long)z * p.sy + eo;
+        if (vec8 && full) {
+          const uint4 t = *reinterpret_cast<const uint4*>(rp);
+          const uint32_t tw[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+          for (int d = 0; d < 4; ++d) rr[2 * d] = tw[d] & 0xffffu, rr[2 * d + 1] = tw[d] >> 16;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (ow0 + e < p.OW) rr[e] = rp[e];
+        }
+      }
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x = apply_act(p.act, v[e] + bias);
+        if constexpr (CL) x = fminf(fmaxf(x, p.cmin), p.cmax);
+        if constexpr (RS) x = p.rcs * x + p.rrs * to_f<DT>(rr[e]);
+        h[e] = from_f<DT>(x);
+      }
+      if (vec8 && full) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+      } else if (vec4) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        if (ow0 + 4 < p.OW) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (ow0 + e < p.OW) dst[e] = (uint16_t)h[e];
+      }
+    };
+    auto grp = [&](const f32x16& x, int g) { return make_float4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]); };
+    if (W == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int gp = 0; gp < 2; ++gp) store_rows(i, j, gp, grp(acc[i][j], 2 * gp), grp(acc[i][j], 2 * gp + 1));
+    } else {
+      auto sum = [&](int q) {
+        float4 v = reinterpret_cast<const float4*>(part)[q * 64 + lane];
+        for (int w = 1; w < W; ++w) {
+          const float4 u = reinterpret_cast<const float4*>(part)[(w * NG + q) * 64 + lane];
+          v.x += u.x;
+          v.y += u.y;
+          v.z += u.z;
+          v.w += u.w;
+        }
+        return v;
+      };
+      // group pairs (2 qp, 2 qp + 1) over the waves
+      for (int qp = wave; qp < NG / 2; qp += W) {
+        const int i = qp / (TN * 2), j = (qp >> 1) % TN, gp = qp & 1;
+        store_rows(i, j, gp, sum(2 * qp), sum(2 * qp + 1));
+      }
+    }
+    return;
+  }
+  const bool vec = (p.OW & 3) == 0;
   auto store_group = [&](int q, float4 v) {
     const int i = q / (TN * 4), j = (q >> 2) % TN, g = q & 3;
     const int oc = m0 + i * 32 + fr, oh = oh0 + 4 * j + g, ow = ow0 + 4 * fc;
@@ -206,7 +298,7 @@ __device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM
     // the residual's elements at the output's positions, read by the lane
     // that writes them (a residual that is the output itself is fine)
     uint32_t rr[4] = {0u, 0u, 0u, 0u};
-    if (p.res) {
+    if constexpr (RS) {
       const char* rsrc_p = static_cast<const char*>(p.res) + ((long long)z * p.sy + eo) * ES;
       if (vec && ow + 3 < p.OW) {
         if constexpr (ES == 4) {
@@ -227,8 +319,8 @@ __device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float x = apply_act(p.act, vv[e]);
-      if (p.has_clamp) x = fminf(fmaxf(x, p.cmin), p.cmax);
-      if (p.res) x = p.rcs * x + p.rrs * to_f<DT>(rr[e]);
+      if constexpr (CL) x = fminf(fmaxf(x, p.cmin), p.cmax);
+      if constexpr (RS) x = p.rcs * x + p.rrs * to_f<DT>(rr[e]);
       h[e] = from_f<DT>(x);
     }
     if (vec && ow + 3 < p.OW) {
@@ -264,6 +356,18 @@ __device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM
       }
       store_group(q, v);
     }
+  }
+}
+
+template <int DT, int TM, int TN>
+__device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM][TN], char* lds, int W, int wave,
+                                              int lane, int m0, int oh0, int ow0, int z, const float (&brow)[TM]) {
+  if (p.has_clamp) {
+    if (p.res) conv_epilogue_t<DT, TM, TN, true, true>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+    else conv_epilogue_t<DT, TM, TN, true, false>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+  } else {
+    if (p.res) conv_epilogue_t<DT, TM, TN, false, true>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+    else conv_epilogue_t<DT, TM, TN, false, false>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
   }
 }
 
@@ -577,6 +681,8 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   using G = GeoCL<KH, KW, S, TN>;
   constexpr int T = G::T, NBLK = G::NBLK;
   constexpr int RING = 3;
+  // the next chunk's tap t + RING - T takes the slot tap t just left
+  static_assert(T % RING == 0, "the weight ring must divide the tap count");
   constexpr int NL = T;  // 16-byte weight loads per row block per chunk (8 channels x T taps)
   extern __shared__ uint4 lds_u4[];
   char* lds = reinterpret_cast<char*>(lds_u4);
@@ -625,12 +731,15 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
       vw[e] = q < G::PHW ? G::row(pr) + G::slot(pc) * 32 : -1;
     }
   }
-  // RV task q = e*64 + lane: channel half q & 1, patch row r = (q/2) / NSEG,
-  // segment g = (q/2) % NSEG at image column a0 + 8g (a0: iw0 rounded down
-  // to a multiple of 8, so a segment lies wholly inside or outside the
-  // image); sp: its input offset in channel 0 of the chunk (OOB outside),
-  // sr: LDS offset of its row and channel half (-1: no task), sg: the patch
-  // column of its first pixel
+  // RV task q = e*64 + lane: segment g = q % NSEG at image column a0 + 8g
+  // (a0: iw0 rounded down to a multiple of 8, so a segment lies wholly
+  // inside or outside the image), channel half h = (q / NSEG) & 1, patch row
+  // r = q / (2 NSEG).  Segments vary fastest: neighbouring lanes load
+  // neighbouring 16 bytes of one channel row, which the address unit takes
+  // as one run (neighbours in different channel planes cost it one cycle
+  // pair each).  sp: its input offset in channel 0 of the chunk (OOB
+  // outside), sr: LDS offset of its row and channel half (-1: no task), sg:
+  // the patch column of its first pixel
   constexpr int NS = RV ? G::NPASS : 1;
   uint32_t sp[NS];
   int sr[NS], sg[NS];
@@ -638,8 +747,8 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
     const int a0 = iw0 - (((iw0 % 8) + 8) % 8), dl = iw0 - a0;
 #pragma unroll
     for (int e = 0; e < G::NPASS; ++e) {
-      const int q = e * 64 + lane, h = q & 1, rs = q >> 1;
-      const int r = rs / G::NSEG, g = rs - r * G::NSEG;
+      const int q = e * 64 + lane, rh = q / G::NSEG, g = q - rh * G::NSEG;
+      const int h = rh & 1, r = rh >> 1;
       const int ih = ih0 + r, s0 = a0 + 8 * g;
       const bool ok = q < G::NTASK;
       sp[e] = (ok && ih >= 0 && ih < p.IH && s0 >= 0 && s0 < p.IW)

@@ -14,7 +14,10 @@ namespace wgx {
 // SiLU is x * sigmoid(x) = x / (1 + e^-x), in float32 before the one
 // rounding to the storage type.
 __device__ __forceinline__ float apply_act(int act, float x) {
-  return act == WGX_ACT_SILU ? x / (1.0f + __expf(-x)) : x;
+  // x * (1 / (1 + e^-x)) with the hardware reciprocal (1 ulp), not an IEEE
+  // division (about a dozen instructions); -0 for large negative x (the
+  // denominator overflows to inf), NaN propagates
+  return act == WGX_ACT_SILU ? x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)) : x;
 }
 
 // Passing this stream to a launch_* function selects the kernel, fills *name
