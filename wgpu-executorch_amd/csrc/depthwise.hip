@@ -349,82 +349,92 @@ __global__ __launch_bounds__(NT) void k_dw_fast(DwFast p) {
   }
   __syncthreads();
 
-  // 3. outputs: item = (plane, output row, segment of OV columns)
-  const uint32_t items_pp = (uint32_t)(rows_here * p.segs);
-  const uint32_t items = (uint32_t)nloc * items_pp;
-  for (uint32_t i = tid; i < items; i += NT) {
-    const uint32_t pp = p.multi ? fdiv(i, p.fd_items) : 0u;
-    const uint32_t rem = i - pp * items_pp;
-    const uint32_t orow = fdiv(rem, p.fd_segs);
-    const int ow0 = (int)(rem - orow * p.segs) * OV;
-    const float* src = tile + pp * p.PLANE + orow * S * p.LW + ow0 * S;
-    const float* wp = wl + pp * WST;
-    float wv[WST];
-#pragma unroll
-    for (int q = 0; q < WST / 4; ++q) {
-      const float4 t = reinterpret_cast<const float4*>(wp)[q];
-      wv[4 * q] = t.x;
-      wv[4 * q + 1] = t.y;
-      wv[4 * q + 2] = t.z;
-      wv[4 * q + 3] = t.w;
-    }
-    float acc[OV];
-#pragma unroll
-    for (int o = 0; o < OV; ++o) acc[o] = wv[KK];
-#pragma unroll
-    for (int kh = 0; kh < K; ++kh) {
-      float win[NW4 * 4];
-#pragma unroll
-      for (int q = 0; q < NW4; ++q) {
-        const float4 t = reinterpret_cast<const float4*>(src + kh * p.LW)[q];
-        win[4 * q] = t.x;
-        win[4 * q + 1] = t.y;
-        win[4 * q + 2] = t.z;
-        win[4 * q + 3] = t.w;
+  // 3. outputs: item = (plane, output row, segment of OV columns) (one instantiation
+  //    per clamp / residual: no per-output selects)
+  auto outputs = [&]<bool CL, bool RS>() {
+    const uint32_t items_pp = (uint32_t)(rows_here * p.segs);
+    const uint32_t items = (uint32_t)nloc * items_pp;
+    for (uint32_t i = tid; i < items; i += NT) {
+      const uint32_t pp = p.multi ? fdiv(i, p.fd_items) : 0u;
+      const uint32_t rem = i - pp * items_pp;
+      const uint32_t orow = fdiv(rem, p.fd_segs);
+      const int ow0 = (int)(rem - orow * p.segs) * OV;
+      const float* src = tile + pp * p.PLANE + orow * S * p.LW + ow0 * S;
+      const float* wp = wl + pp * WST;
+      float wv[WST];
+  #pragma unroll
+      for (int q = 0; q < WST / 4; ++q) {
+        const float4 t = reinterpret_cast<const float4*>(wp)[q];
+        wv[4 * q] = t.x;
+        wv[4 * q + 1] = t.y;
+        wv[4 * q + 2] = t.z;
+        wv[4 * q + 3] = t.w;
       }
-#pragma unroll
-      for (int kw = 0; kw < K; ++kw)
-#pragma unroll
-        for (int o = 0; o < OV; ++o) acc[o] = fmaf(win[o * S + kw], wv[kh * K + kw], acc[o]);
-    }
-    const long long yo = ((long long)(plane0 + pp) * p.OH + oh0 + orow) * p.OW + ow0;
-    uint32_t h[OV];
-#pragma unroll
-    for (int o = 0; o < OV; ++o) {
-      float v = acc[o];
-      v = apply_act(p.act, v);
-      if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
-      if (p.res && ow0 + o < p.OW) v = p.rcs * v + p.rrs * ldv<DT>(p.res, yo + o);
-      h[o] = to_bits<DT>(v);
-    }
-    char* yp = static_cast<char*>(p.y) + yo * ES;
-    const uintptr_t ya = reinterpret_cast<uintptr_t>(yp);
-    if (ow0 + OV <= p.OW && (ya & 15) == 0 && (OV * ES) % 16 == 0) {
-#pragma unroll
-      for (int q = 0; q < OV * ES / 16; ++q) {
-        uint4 t;
-        if constexpr (ES == 4) t = make_uint4(h[4 * q], h[4 * q + 1], h[4 * q + 2], h[4 * q + 3]);
-        else
-          t = make_uint4(h[8 * q] | (h[8 * q + 1] << 16), h[8 * q + 2] | (h[8 * q + 3] << 16),
-                         h[8 * q + 4] | (h[8 * q + 5] << 16), h[8 * q + 6] | (h[8 * q + 7] << 16));
-        using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
-        __builtin_nontemporal_store(u32x4{t.x, t.y, t.z, t.w}, reinterpret_cast<u32x4*>(yp) + q);
+      float acc[OV];
+  #pragma unroll
+      for (int o = 0; o < OV; ++o) acc[o] = wv[KK];
+  #pragma unroll
+      for (int kh = 0; kh < K; ++kh) {
+        float win[NW4 * 4];
+  #pragma unroll
+        for (int q = 0; q < NW4; ++q) {
+          const float4 t = reinterpret_cast<const float4*>(src + kh * p.LW)[q];
+          win[4 * q] = t.x;
+          win[4 * q + 1] = t.y;
+          win[4 * q + 2] = t.z;
+          win[4 * q + 3] = t.w;
+        }
+  #pragma unroll
+        for (int kw = 0; kw < K; ++kw)
+  #pragma unroll
+          for (int o = 0; o < OV; ++o) acc[o] = fmaf(win[o * S + kw], wv[kh * K + kw], acc[o]);
       }
-    } else if (ow0 + OV <= p.OW && (ya & 7) == 0 && OV * ES == 8) {
-      uint2 t;
-      if constexpr (ES == 4) t = make_uint2(h[0], h[1]);
-      else t = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-      using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
-      __builtin_nontemporal_store(u32x2{t.x, t.y}, reinterpret_cast<u32x2*>(yp));
-    } else {
-#pragma unroll
+      const long long yo = ((long long)(plane0 + pp) * p.OH + oh0 + orow) * p.OW + ow0;
+      uint32_t h[OV];
+  #pragma unroll
       for (int o = 0; o < OV; ++o) {
-        if (ow0 + o < p.OW) {
-          if constexpr (ES == 4) reinterpret_cast<uint32_t*>(yp)[o] = h[o];
-          else reinterpret_cast<uint16_t*>(yp)[o] = (uint16_t)h[o];
+        float v = acc[o];
+        v = apply_act(p.act, v);
+        if constexpr (CL) v = fminf(fmaxf(v, p.cmin), p.cmax);
+        if (RS && ow0 + o < p.OW) v = p.rcs * v + p.rrs * ldv<DT>(p.res, yo + o);
+        h[o] = to_bits<DT>(v);
+      }
+      char* yp = static_cast<char*>(p.y) + yo * ES;
+      const uintptr_t ya = reinterpret_cast<uintptr_t>(yp);
+      if (ow0 + OV <= p.OW && (ya & 15) == 0 && (OV * ES) % 16 == 0) {
+  #pragma unroll
+        for (int q = 0; q < OV * ES / 16; ++q) {
+          uint4 t;
+          if constexpr (ES == 4) t = make_uint4(h[4 * q], h[4 * q + 1], h[4 * q + 2], h[4 * q + 3]);
+          else
+            t = make_uint4(h[8 * q] | (h[8 * q + 1] << 16), h[8 * q + 2] | (h[8 * q + 3] << 16),
+                           h[8 * q + 4] | (h[8 * q + 5] << 16), h[8 * q + 6] | (h[8 * q + 7] << 16));
+          using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+          __builtin_nontemporal_store(u32x4{t.x, t.y, t.z, t.w}, reinterpret_cast<u32x4*>(yp) + q);
+        }
+      } else if (ow0 + OV <= p.OW && (ya & 7) == 0 && OV * ES == 8) {
+        uint2 t;
+        if constexpr (ES == 4) t = make_uint2(h[0], h[1]);
+        else t = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+        __builtin_nontemporal_store(u32x2{t.x, t.y}, reinterpret_cast<u32x2*>(yp));
+      } else {
+  #pragma unroll
+        for (int o = 0; o < OV; ++o) {
+          if (ow0 + o < p.OW) {
+            if constexpr (ES == 4) reinterpret_cast<uint32_t*>(yp)[o] = h[o];
+            else reinterpret_cast<uint16_t*>(yp)[o] = (uint16_t)h[o];
+          }
         }
       }
     }
+  };
+  if (p.has_clamp) {
+    if (p.res) outputs.template operator()<true, true>();
+    else outputs.template operator()<true, false>();
+  } else {
+    if (p.res) outputs.template operator()<false, true>();
+    else outputs.template operator()<false, false>();
   }
 }
 
@@ -664,37 +674,47 @@ __global__ __launch_bounds__(64) void k_dw_reg(DwReg p) {
     }
   }
 
-  // 4. stores: OV halves per output row, one vector store when whole
+  // 4. stores: OV halves per output row, one vector store when whole (one
+  //    instantiation per clamp / residual: no per-output selects)
   if (!active) return;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int oh = oh0 + r;
-    if (oh >= p.OH) break;
-    uint32_t h[OV];
-#pragma unroll
-    for (int o = 0; o < OV; ++o) {
-      float v = acc[r][o];
-      v = apply_act(p.act, v);
-      if (p.has_clamp) v = fminf(fmaxf(v, p.cmin), p.cmax);
-      if (p.res) v = p.rcs * v + p.rrs * ((o & 1) ? hi_f(rres[r][o / 2]) : lo_f(rres[r][o / 2]));
-      h[o] = __builtin_bit_cast(uint16_t, (_Float16)v);
-    }
-    const uint32_t off = (uint32_t)(((ps * p.OH + oh) * p.OW + seg * OV) * 2);
-    if (nvalid == OV) {
-      if constexpr (OV == 8) {
-        using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
-        const u32x4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-        __builtin_amdgcn_raw_buffer_store_b128(v, ry, (int)off, 0, kStoreNT);
-      } else {
-        using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
-        const u32x2 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-        __builtin_amdgcn_raw_buffer_store_b64(v, ry, (int)off, 0, kStoreNT);
+  auto stores = [&]<bool CL, bool RS>() {
+  #pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int oh = oh0 + r;
+      if (oh >= p.OH) break;
+      uint32_t h[OV];
+  #pragma unroll
+      for (int o = 0; o < OV; ++o) {
+        float v = acc[r][o];
+        v = apply_act(p.act, v);
+        if constexpr (CL) v = fminf(fmaxf(v, p.cmin), p.cmax);
+        if constexpr (RS) v = p.rcs * v + p.rrs * ((o & 1) ? hi_f(rres[r][o / 2]) : lo_f(rres[r][o / 2]));
+        h[o] = __builtin_bit_cast(uint16_t, (_Float16)v);
       }
-    } else {
-#pragma unroll
-      for (int o = 0; o < OV; ++o)
-        if (o < nvalid) __builtin_amdgcn_raw_buffer_store_b16((unsigned short)h[o], ry, (int)(off + 2 * o), 0, kStoreNT);
+      const uint32_t off = (uint32_t)(((ps * p.OH + oh) * p.OW + seg * OV) * 2);
+      if (nvalid == OV) {
+        if constexpr (OV == 8) {
+          using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+          const u32x4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+          __builtin_amdgcn_raw_buffer_store_b128(v, ry, (int)off, 0, kStoreNT);
+        } else {
+          using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+          const u32x2 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+          __builtin_amdgcn_raw_buffer_store_b64(v, ry, (int)off, 0, kStoreNT);
+        }
+      } else {
+  #pragma unroll
+        for (int o = 0; o < OV; ++o)
+          if (o < nvalid) __builtin_amdgcn_raw_buffer_store_b16((unsigned short)h[o], ry, (int)(off + 2 * o), 0, kStoreNT);
+      }
     }
+  };
+  if (p.has_clamp) {
+    if (p.res) stores.template operator()<true, true>();
+    else stores.template operator()<true, false>();
+  } else {
+    if (p.res) stores.template operator()<false, true>();
+    else stores.template operator()<false, false>();
   }
 }
 
