@@ -1000,11 +1000,23 @@ hipError_t launch_dt(const CParams& p, const Cfg& c, int S, unsigned grid, hipSt
   }
 }
 
-// The channel-last 64 x (32 TN) one-wave tile on pre-ordered weights: the
-// reorder pass into d.wpre, then the kernel reading them.
-template <int DT, bool RV, int TN, int S>
-hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned grid, hipStream_t s) {
-  auto fn = k_conv_cl<DT, 3, 3, S, 2, TN, RV, true>;
+// LDS bytes of a channel-last block of W waves: their patches, or the
+// partial sums of their reduction, whichever is larger.
+template <int S, int TM, int TN>
+size_t cl_block_lds(int W) {
+  const size_t patch = (size_t)W * GeoCL<3, 3, S, TN>::LDS_WAVE;
+  const size_t part = W > 1 ? (size_t)W * TM * TN * 4 * 64 * 16 : 0;
+  return patch > part ? patch : part;
+}
+
+// The channel-last tile on pre-ordered weights: the reorder pass into wpre,
+// then the kernel reading them, in blocks of W waves.
+template <int DT, bool RV, int TM, int TN, int S>
+hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned grid, int W, hipStream_t s) {
+  const size_t lds = cl_block_lds<S, TM, TN>(W);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  if (is_dry(s)) return hipSuccess;
+  auto fn = k_conv_cl<DT, 3, 3, S, TM, TN, RV, true>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -1020,9 +1032,34 @@ hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned g
   if (e != hipSuccess) return e;
   CParams q = p;
   q.w = wpre;
-  const size_t lds = (size_t)GeoCL<3, 3, S, TN>::LDS_WAVE;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(64), lds, s, q);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, s, q);
   return hipGetLastError();
+}
+
+// The tiles that run on pre-ordered weights: 64 x 64 one-wave (either
+// stride) and 64 x 128 one-wave (stride 1).  The batch-1 split-chunk tiles
+// keep the raw weights: on them the kernel gains (32 x 64 s1 [1,64,80,80]
+// -> 128: 7.6 us, 64 x 32 s2 [1,128,80,80] -> 256: 8.5 us), but the reorder
+// launch (4.4 us) costs more than that in a graph of batch-1 launches
+// (10.0 / 11.5 us against 9.1 / 12.5 us amortised; [1,256,20,20] -> 256:
+// 17.7 against 12.4 us).
+bool pre_form(const Cfg& c, int S) {
+  return c.cl && c.tm == 2 && c.w == 1 && (c.tn == 2 || (c.tn == 4 && S == 1));
+}
+
+template <int DT>
+hipError_t launch_pre_dt(const CParams& p, const Cfg& c, int S, const void* w, void* wpre, unsigned grid,
+                         hipStream_t s) {
+  if (c.tm == 2 && c.tn == 2 && S == 2)
+    return c.rv ? launch_cl_pre<DT, true, 2, 2, 2>(p, w, wpre, grid, c.w, s)
+                : launch_cl_pre<DT, false, 2, 2, 2>(p, w, wpre, grid, c.w, s);
+  if (c.tm == 2 && c.tn == 2)
+    return c.rv ? launch_cl_pre<DT, true, 2, 2, 1>(p, w, wpre, grid, c.w, s)
+                : launch_cl_pre<DT, false, 2, 2, 1>(p, w, wpre, grid, c.w, s);
+  if (c.tm == 2 && c.tn == 4 && S == 1)
+    return c.rv ? launch_cl_pre<DT, true, 2, 4, 1>(p, w, wpre, grid, c.w, s)
+                : launch_cl_pre<DT, false, 2, 4, 1>(p, w, wpre, grid, c.w, s);
+  return hipErrorInvalidValue;
 }
 
 // Input channels per chunk: 8 for float32 (the channel-major kernel's lane
@@ -1137,10 +1174,12 @@ CParams make_params(const ConvLdsDesc& d, const Cfg& c) {
 // Images whose rows are whole 16-byte segments on a 16-byte base (float32: a
 // multiple of 4 columns, 16-bit: of 8) load the patch as row segments;
 // WGX_CONV_RV=0 keeps the element loads.
-bool use_rv(const ConvLdsDesc& d, const Cfg& c) {
+// (the channel-last 64 x 32 tile takes row segments on pre-ordered weights
+// only: with the raw weights' registers it would spill)
+bool use_rv(const ConvLdsDesc& d, const Cfg& c, bool pre) {
   const bool rv_off = getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0;
   return d.IW % (d.dtype == WGX_FLOAT32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
-         (d.dtype == WGX_FLOAT32 || (c.cl && !(c.tm == 2 && c.tn == 1))) && !rv_off;
+         (d.dtype == WGX_FLOAT32 || (c.cl && (pre || !(c.tm == 2 && c.tn == 1)))) && !rv_off;
 }
 
 template <int SA, bool RVA, int SB, bool RVB>
@@ -1183,24 +1222,22 @@ bool conv_lds_applies(const ConvLdsDesc& d) {
   return true;
 }
 
-// The channel-last one-wave 64 x 64 tile (either stride) and 64 x 128 tile
-// (stride 1) -- the batched 16-bit choice -- run on weights pre-ordered by a
-// small pass into a workspace of OC * IC * 9 elements (WGX_CONV_PRE=0: on
-// the raw weights).
+// The channel-last tiles of pre_form (the batched 16-bit choice) run on
+// weights pre-ordered by a small pass into a workspace of OC * IC * 9
+// elements (WGX_CONV_PRE=0: on the raw weights).
 bool conv_lds_wants_prepass(const ConvLdsDesc& d, int cus) {
   if (getenv("WGX_CONV_PRE") && strcmp(getenv("WGX_CONV_PRE"), "0") == 0) return false;
   if (!conv_lds_applies(d) || d.dtype == WGX_FLOAT32 || d.KH != 3 || d.KW != 3) return false;
-  const Cfg c = choose(d, cus);
-  return c.cl && c.tm == 2 && c.w == 1 && (c.tn == 2 || (c.tn == 4 && d.sH == 1));
+  return pre_form(choose(d, cus), d.sH);
 }
 
 hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::string* name) {
   if (!conv_lds_applies(d)) return hipErrorNotSupported;
   Cfg c = choose(d, cus);
   if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
-  c.rv = use_rv(d, c);
+  const bool pre = d.wpre && pre_form(c, d.sH);
+  c.rv = use_rv(d, c, pre);
   const CParams p = make_params(d, c);
-  const bool pre = d.wpre && c.cl && c.tm == 2 && c.w == 1 && (c.tn == 2 || (c.tn == 4 && d.sH == 1));
   if (name) {
     char buf[96];
     snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d%s", c.cl ? "cl" : "lds",
@@ -1211,27 +1248,8 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   if (p.ntiles == 0) return hipSuccess;
   const unsigned grid = (unsigned)p.ntiles;
   if (pre) {
-    if (is_dry(s)) return hipSuccess;
-    const bool bf = d.dtype == WGX_BFLOAT16;
-    if (c.tn == 2 && d.sH == 2) {
-      if (bf)
-        return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 2, 2>(p, d.w, d.wpre, grid, s)
-                    : launch_cl_pre<WGX_BFLOAT16, false, 2, 2>(p, d.w, d.wpre, grid, s);
-      return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 2, 2>(p, d.w, d.wpre, grid, s)
-                  : launch_cl_pre<WGX_FLOAT16, false, 2, 2>(p, d.w, d.wpre, grid, s);
-    }
-    if (c.tn == 2) {
-      if (bf)
-        return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 2, 1>(p, d.w, d.wpre, grid, s)
-                    : launch_cl_pre<WGX_BFLOAT16, false, 2, 1>(p, d.w, d.wpre, grid, s);
-      return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 2, 1>(p, d.w, d.wpre, grid, s)
-                  : launch_cl_pre<WGX_FLOAT16, false, 2, 1>(p, d.w, d.wpre, grid, s);
-    }
-    if (bf)
-      return c.rv ? launch_cl_pre<WGX_BFLOAT16, true, 4, 1>(p, d.w, d.wpre, grid, s)
-                  : launch_cl_pre<WGX_BFLOAT16, false, 4, 1>(p, d.w, d.wpre, grid, s);
-    return c.rv ? launch_cl_pre<WGX_FLOAT16, true, 4, 1>(p, d.w, d.wpre, grid, s)
-                : launch_cl_pre<WGX_FLOAT16, false, 4, 1>(p, d.w, d.wpre, grid, s);
+    if (d.dtype == WGX_BFLOAT16) return launch_pre_dt<WGX_BFLOAT16>(p, c, d.sH, d.w, d.wpre, grid, s);
+    return launch_pre_dt<WGX_FLOAT16>(p, c, d.sH, d.w, d.wpre, grid, s);
   }
   if (d.dtype == WGX_FLOAT32) return launch_dt<WGX_FLOAT32>(p, c, d.sH, grid, s);
   if (d.dtype == WGX_BFLOAT16) return launch_dt<WGX_BFLOAT16>(p, c, d.sH, grid, s);
@@ -1253,8 +1271,8 @@ hipError_t launch_conv_lds_pair(const ConvLdsDesc& a, const ConvLdsDesc& b, int 
   // 4 waves per block for both (headline step, paired: 32 us at 4 waves,
   // 40 at 2, 55 at 1; 35.5 us as two launches)
   ca.w = cb.w = 4;
-  ca.rv = use_rv(a, ca);
-  cb.rv = use_rv(b, cb);
+  ca.rv = use_rv(a, ca, false);
+  cb.rv = use_rv(b, cb, false);
   const CParams pa = make_params(a, ca), pb = make_params(b, cb);
   if (pa.ntiles == 0 || pb.ntiles == 0 || (long long)pa.ntiles + pb.ntiles >= (1LL << 31)) return hipErrorNotSupported;
   if (is_dry(s)) return hipSuccess;
