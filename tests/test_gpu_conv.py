@@ -365,6 +365,9 @@ DENSE_RESIDUAL_CASES = [
     ((1, 64, 24, 24), (64, 64, 3, 3), 1, 1, (1.0, 1.0), True, None),      # residual is the output
     ((1, 32, 17, 13), (24, 32, 3, 3), 1, 1, (1.0, 2.0), False, "2x2w4"),  # W > 1, ragged edges
     ((2, 32, 16, 32), (64, 32, 3, 3), 1, 1, (1.0, 1.0), True, "2x4w1"),   # the 64 x 128 tile, in place
+    ((1, 32, 12, 20), (40, 32, 3, 3), 1, 1, (1.0, -0.5), False, None),    # width 20: 8-byte row pieces
+    ((2, 32, 16, 16), (64, 32, 3, 3), 1, 1, (0.5, 1.0), False, "2x2w1"),  # 64 x 64 tile (pre-ordered, 16-bit)
+    ((2, 32, 18, 16), (64, 32, 3, 3), 2, 1, (1.0, 1.0), False, "2x2w1"),  # the same at stride 2
 ]
 
 
@@ -702,3 +705,50 @@ def test_bfloat16_convolution_routes(gpu_ctx, orc, pkg, monkeypatch, case):
     got, kernel = run_conv(gpu_ctx, x, w, b, "bfloat16", (s, s), (p, p), out_shape=list(ref.shape))
     assert kernel.startswith(want), kernel
     assert_parity(got, ref, refa, "bfloat16", ws[1] * ws[2] * ws[3], f"bf16 route {case} {xs}x{ws} s{s} {kernel}")
+
+
+# clamp and residual in one launch (the epilogues are instantiated per clamp /
+# residual pair): out = cs * clamp(silu(conv)) + rs * residual, on the dense
+# LDS-patch kernels (8-byte row pieces at width 20, the pre-ordered 64 x 64
+# tile at both strides, W > 1 with ragged edges) and the depthwise kernels
+CLAMP_RES_CASES = [
+    ((1, 32, 12, 20), (40, 32, 3, 3), 1, 1, 1, None),
+    ((2, 32, 16, 16), (64, 32, 3, 3), 1, 1, 1, "2x2w1"),
+    ((2, 32, 18, 16), (64, 32, 3, 3), 2, 1, 1, "2x2w1"),
+    ((1, 32, 17, 13), (24, 32, 3, 3), 1, 1, 1, "2x2w4"),
+    ((2, 48, 20, 20), (48, 1, 3, 3), 1, 1, 48, None),
+    ((2, 64, 20, 20), (64, 1, 5, 5), 2, 2, 64, None),
+]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_conv_clamp_and_residual(gpu_ctx, orc, pkg, monkeypatch, dtype):
+    """SiLU, a clamp and a residual together against the float64 convolution
+    (the clamp is 1-Lipschitz, so the SiLU bound carries through it)."""
+    W, I = pkg.wgx, pkg.inputs
+    cs, rs, lo, hi = 0.5, -1.0, -0.25, 0.5
+    for i, (xs, ws, s, p, g, cfg) in enumerate(CLAMP_RES_CASES):
+        if cfg is not None:
+            monkeypatch.setenv("WGX_CONV_LDS", cfg)
+        else:
+            monkeypatch.delenv("WGX_CONV_LDS", raising=False)
+        x = round_in(I.uniform(4400 + i, xs, -1, 1), dtype)
+        w = round_in(I.uniform(4410 + i, ws, -0.5, 0.5), dtype)
+        b = round_in(I.uniform(4420 + i, (ws[0],), -0.5, 0.5), dtype)
+        ref, refa = orc.conv2d_f64(x, w, b, (s, s), (p, p), (1, 1), g)
+        r = round_in(I.uniform(4430 + i, ref.shape, -2, 2), dtype)
+        tx, tw, tb = gpu_ctx.from_numpy(x, dtype), gpu_ctx.from_numpy(w, dtype), gpu_ctx.from_numpy(b, dtype)
+        tr = gpu_ctx.from_numpy(r, dtype)
+        ty = gpu_ctx.tensor(dtype, list(ref.shape))
+        gpu_ctx.reset()
+        gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], g, ty, clamp=(lo, hi),
+                            activation=W.ACT_SILU, residual=tr, conv_scale=cs, residual_scale=rs)
+        kernel = gpu_ctx.last_kernel
+        if cfg == "2x2w1" and dtype != "float32":
+            assert kernel.endswith("_pre"), kernel
+        gpu_ctx.submit()
+        gpu_ctx.sync()
+        want = cs * np.clip(ref / (1.0 + np.exp(-ref)), lo, hi) + rs * r.astype(np.float64)
+        bound = 1.1 * abs(cs) * refa + abs(rs) * np.abs(r.astype(np.float64))
+        assert_parity(ty.get_f32(), want, bound, dtype, ws[1] * ws[2] * ws[3],
+                      f"clamp+residual case {i} {dtype} {xs}x{ws} s{s} g{g} {kernel}")
