@@ -575,6 +575,8 @@ CL_SEG_CASES = [
     ((1, 32, 12, 24), (8, 32, 3, 3), 2, 2),
     ((1, 16, 3, 8), (33, 16, 3, 3), 1, 1),
     ((1, 32, 17, 40), (64, 32, 3, 3), 2, 0),
+    ((1, 32, 12, 16), (200, 32, 3, 3), 1, 1),   # pre-ordered: 4 output-channel tiles share a patch
+    ((2, 16, 14, 24), (150, 16, 3, 3), 2, 1),   # 3 share, stride 2
 ]
 
 
@@ -713,8 +715,8 @@ def test_bfloat16_convolution_routes(gpu_ctx, orc, pkg, monkeypatch, case):
 # tile at both strides, W > 1 with ragged edges) and the depthwise kernels
 CLAMP_RES_CASES = [
     ((1, 32, 12, 20), (40, 32, 3, 3), 1, 1, 1, None),
-    ((2, 32, 16, 16), (64, 32, 3, 3), 1, 1, 1, "2x2w1"),
-    ((2, 32, 18, 16), (64, 32, 3, 3), 2, 1, 1, "2x2w1"),
+    ((2, 32, 16, 16), (256, 32, 3, 3), 1, 1, 1, "2x2w1"),
+    ((2, 32, 18, 16), (128, 32, 3, 3), 2, 1, 1, "2x2w1"),
     ((1, 32, 17, 13), (24, 32, 3, 3), 1, 1, 1, "2x2w4"),
     ((2, 48, 20, 20), (48, 1, 3, 3), 1, 1, 48, None),
     ((2, 64, 20, 20), (64, 1, 5, 5), 2, 2, 64, None),

@@ -87,6 +87,10 @@ struct CParams {
   float cmin, cmax;
   const void* res;  // output-shaped residual or null: y = rcs * y + rrs * res
   float rcs, rrs;
+  // waves of a block that share one input patch, each on its own output-
+  // channel tile of the same pixels (the channel-last kernel on pre-ordered
+  // weights with row segments; 1 otherwise)
+  int share;
 };
 
 template <int DT>
@@ -691,12 +695,18 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = p.W;
   const int fr = lane & 31, fc = lane >> 5;
+  // SHW > 1 (pre-ordered weights, row segments, W = 1): the block's waves take
+  // output-channel tiles tmb*SHW + wave of one pixel tile and load one shared
+  // patch between them, each wave a contiguous share of its segment tasks
+  const int SHW = (PRE && RV) ? p.share : 1;
+  const int sw = SHW > 1 ? wave : 0;
   // XCD-aware numbering, output-channel tiles fastest (as in k_conv_lds)
   const int Gn = gridDim.x;
   const int rb = (Gn & 7) == 0 ? (blockIdx.x & 7) * (Gn >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int mtb = (p.tiles_m + SHW - 1) / SHW;
   int t0 = rb;
-  const int tm = t0 % p.tiles_m;
-  t0 /= p.tiles_m;
+  const int tm = (t0 % mtb) * SHW + sw;
+  t0 /= mtb;
   const int tw = t0 % p.tiles_w;
   t0 /= p.tiles_w;
   const int th = t0 % p.tiles_h;
@@ -743,14 +753,16 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   constexpr int NS = RV ? G::NPASS : 1;
   uint32_t sp[NS];
   int sr[NS], sg[NS];
+  // tasks per wave: all of them, or a contiguous share of a shared patch
+  const int qpw = (G::NTASK + SHW - 1) / SHW;
   if constexpr (RV) {
     const int a0 = iw0 - (((iw0 % 8) + 8) % 8), dl = iw0 - a0;
 #pragma unroll
     for (int e = 0; e < G::NPASS; ++e) {
-      const int q = e * 64 + lane, rh = q / G::NSEG, g = q - rh * G::NSEG;
+      const int ql = e * 64 + lane, q = sw * qpw + ql, rh = q / G::NSEG, g = q - rh * G::NSEG;
       const int h = rh & 1, r = rh >> 1;
       const int ih = ih0 + r, s0 = a0 + 8 * g;
-      const bool ok = q < G::NTASK;
+      const bool ok = ql < qpw && q < G::NTASK;
       sp[e] = (ok && ih >= 0 && ih < p.IH && s0 >= 0 && s0 < p.IW)
                   ? (uint32_t)((ih * p.IW + s0) * 2 + h * 8 * plane * 2)
                   : OOB;
@@ -758,7 +770,10 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
       sg[e] = 8 * g - dl;
     }
   }
-  char* wl = lds + wave * G::LDS_WAVE;
+  // a wave's own patch, or (shared) two patch buffers taken in turn by
+  // consecutive chunks
+  char* const wl0 = lds + (SHW > 1 ? 0 : wave * G::LDS_WAVE);
+  char* wl = wl0;
   float brow[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -793,8 +808,10 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
     if constexpr (RV) {
 #pragma unroll
       for (int e = 0; e < G::NPASS; ++e)
+        if (e * 64 < qpw) {
 #pragma unroll
-        for (int ch = 0; ch < 8; ++ch) ps[e][ch] = ld16(rx, sp[e], ch * cplane);
+          for (int ch = 0; ch < 8; ++ch) ps[e][ch] = ld16(rx, sp[e], ch * cplane);
+        }
     } else {
 #pragma unroll
       for (int e = 0; e < NBLK; ++e)
@@ -870,7 +887,7 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
     }
   };
 
-  int c = wave;
+  int c = SHW > 1 ? 0 : wave;
   if (c < p.nchunks) {
     load_patch(c);
     if constexpr (PRE) {
@@ -880,13 +897,18 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
       load_a(c);
     }
   }
-  for (; c < p.nchunks; c += W) {
+  for (int it = 0; c < p.nchunks; c += W, ++it) {
     const bool more = c + W < p.nchunks;
     // the patch -> LDS (the previous chunk's reads came first: a wave's LDS
     // operations run in order), the weights -> fragments, then the next
     // chunk's loads go out behind this chunk's multiplies
+    if (SHW > 1) wl = wl0 + (it & 1) * G::LDS_WAVE;
     store_patch();
     if constexpr (!PRE) build_a();
+    // shared patch: every wave's share is in LDS before any wave reads it
+    // (the buffer written here was last read two chunks ago, before every
+    // wave reached the previous chunk's barrier)
+    if (SHW > 1) __syncthreads();
     asm volatile("" ::: "memory");
     if (more) {
       load_patch(c + W);
@@ -1013,7 +1035,9 @@ size_t cl_block_lds(int W) {
 // then the kernel reading them, in blocks of W waves.
 template <int DT, bool RV, int TM, int TN, int S>
 hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned grid, int W, hipStream_t s) {
-  const size_t lds = cl_block_lds<S, TM, TN>(W);
+  // a shared patch: two buffers for the block (W is 1 then)
+  const size_t lds = p.share > 1 ? 2 * (size_t)GeoCL<3, 3, S, TN>::LDS_WAVE : cl_block_lds<S, TM, TN>(W);
+  const int nw = p.share > 1 ? p.share : W;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   if (is_dry(s)) return hipSuccess;
   auto fn = k_conv_cl<DT, 3, 3, S, TM, TN, RV, true>;
@@ -1032,7 +1056,7 @@ hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned g
   if (e != hipSuccess) return e;
   CParams q = p;
   q.w = wpre;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, s, q);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), lds, s, q);
   return hipGetLastError();
 }
 
@@ -1159,6 +1183,7 @@ CParams make_params(const ConvLdsDesc& d, const Cfg& c) {
   p.tiles_h = (d.OH + 4 * c.tn - 1) / (4 * c.tn);
   p.tiles_w = (d.OW + 7) / 8;
   p.ntiles = d.B * p.tiles_m * p.tiles_h * p.tiles_w;
+  p.share = 1;
   p.nchunks = d.IC / chunk_channels(d.dtype);
   p.W = c.w;
   p.act = d.act;
@@ -1237,7 +1262,20 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
   const bool pre = d.wpre && pre_form(c, d.sH);
   c.rv = use_rv(d, c, pre);
-  const CParams p = make_params(d, c);
+  CParams p = make_params(d, c);
+  if (pre && c.rv && c.w == 1) {
+    // the output-channel tiles of one pixel tile share its patch, in blocks
+    // of the largest of 4, 3, 2 waves that divides their count
+    // (WGX_CONV_SHARE=0: a patch per wave)
+    const char* e = getenv("WGX_CONV_SHARE");
+    if (!(e && strcmp(e, "0") == 0))
+      for (int g = 4; g >= 2; --g)
+        if (p.tiles_m % g == 0) {
+          p.share = g;
+          p.ntiles /= g;
+          break;
+        }
+  }
   if (name) {
     char buf[96];
     snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d%s", c.cl ? "cl" : "lds",
