@@ -211,17 +211,20 @@ def time_ctx(ctx, reps, warm=3):
     return ctx.time_submits(reps)
 
 
-def measure(W, build, n_inst_amortised, reps_shape=50, reps_amort=5):
+def measure(W, build, n_inst_amortised, reps_shape=50, reps_amort=5, graph=True):
     """At-shape: one instance, one launch per submit.  Amortised: a graph of
-    n instances with distinct buffers, per-instance time."""
+    n instances with distinct buffers, per-instance time (graph=False: the
+    instances issued as direct launches, as a short command list runs)."""
     ctx = W.Context(0)
     try:
+        ctx.set_graph_mode(graph)
         kernel = build(ctx, 0)
         shape_ms = time_ctx(ctx, reps_shape)
     finally:
         ctx.destroy()
     ctx = W.Context(0)
     try:
+        ctx.set_graph_mode(graph)
         for i in range(n_inst_amortised):
             build(ctx, i)
         amort_ms = time_ctx(ctx, reps_amort, warm=1) / n_inst_amortised
@@ -520,8 +523,8 @@ def cpu_baseline(I, budget_s=20.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--detail", type=str, default=None, help="write per-config JSON here")
     ap.add_argument("--no-detail", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -582,6 +585,9 @@ def main():
         ctx.submit()
     ctx.sync()
     el = time.perf_counter() - t0
+    # the same steps again between HIP events on the context's stream: the
+    # per-launch time of the step as it runs back to back (operands warm)
+    steps_ms = ctx.time_submits(args.steps)
     # 2a and 2b read and write disjoint buffers: the runtime may run them as
     # one paired launch (WGX_MERGE=0 keeps them apart)
     paired = ctx.paired_launches > 0
@@ -596,6 +602,9 @@ def main():
     #    in all, so the 256 MB MALL cannot hold the working set and every
     #    launch reads its operands from HBM;
     #  warm: 20 launches of one instance (operands stay in L2 / MALL).
+    # Both issue the instances as direct launches, the path a step's short
+    # command list takes (a graph's kernel nodes run slower: the paired
+    # launch 29.2 us in a graph, 26.8 us per step issued directly).
     per_kernel, warm = {}, {}
     reps_in_graph = 20
     if paired:
@@ -604,6 +613,7 @@ def main():
         # amortised: a graph of (2a, 2b) instances over >= 300 MB
         kctx = W.Context(0)
         try:
+            kctx.set_graph_mode(False)
             for _ in range(reps_in_graph):
                 for v, c in CONV2.items():
                     build_conv(kctx, I, c, "float32", 40 + 10 * (v == "2b"))
@@ -615,7 +625,8 @@ def main():
         def build_pair(ctx, i):
             for v, c in CONV2.items():
                 build_conv(ctx, I, c, "float32", 40 + 10 * i + 5 * (v == "2b"))
-        _, _, per_kernel["pair"] = measure(W, build_pair, int(300e6 / pair_bytes) + 1, reps_shape=5, reps_amort=10)
+        _, _, per_kernel["pair"] = measure(W, build_pair, int(300e6 / pair_bytes) + 1, reps_shape=5, reps_amort=10,
+                                           graph=False)
         dom, flops_dom, bytes_dom = "pair", step_flops, pair_bytes
         kname = "k_conv_lds_pair (" + " + ".join(kernels[v] for v in CONV2) + ")"
         covers, wl = "one dispatch: conv 2a and 2b paired", "conv 2a + conv 2b (one paired launch)"
@@ -623,13 +634,14 @@ def main():
         for v, c in CONV2.items():
             kctx = W.Context(0)
             try:
+                kctx.set_graph_mode(False)
                 build_conv(kctx, I, c, "float32", 40, repeat=reps_in_graph)
                 warm[v] = time_ctx(kctx, 20) / reps_in_graph
             finally:
                 kctx.destroy()
             n = int(300e6 / conv_bytes(c, 4)) + 1
             _, _, per_kernel[v] = measure(W, lambda ctx, i, c=c: build_conv(ctx, I, c, "float32", 40 + 10 * i), n,
-                                          reps_shape=5, reps_amort=10)
+                                          reps_shape=5, reps_amort=10, graph=False)
         dom = max(per_kernel, key=per_kernel.get)
         flops_dom, bytes_dom, kname = conv_flops(CONV2[dom]), conv_bytes(CONV2[dom], 4), kernels[dom]
         covers = ("GEMM dispatch + split-K reduction dispatch" if re.search(r"_k\d+$", kernels[dom])
@@ -644,9 +656,13 @@ def main():
                 "traffic": traffic["bytes"] if traffic else None,
                 "kernel": kname, "workload": wl,
                 "launch_us": round(dom_ms * 1e3, 2),
-                "protocol": "amortised: a graph of instances over >= 300 MB of distinct buffers",
+                "protocol": "amortised: direct launches of instances over >= 300 MB of distinct buffers",
                 "frac_warm": round(achieved_warm / PEAK["fp32_TFLOPs"], 4),
                 "launch_us_warm": round(warm[dom] * 1e3, 2),
+                # the timed steps themselves (a step is the one paired launch
+                # when paired; else both launches of the step)
+                "launch_us_steps": round(steps_ms * 1e3, 2),
+                "frac_steps": round(step_flops / (steps_ms * 1e-3) / 1e12 / PEAK["fp32_TFLOPs"], 4),
                 "launch_covers": covers,
                 "algorithmic_bytes": bytes_dom}
     if traffic:
