@@ -234,3 +234,37 @@ def test_shared_contexts_order_and_freed_buffers(pkg):
     finally:
         b.destroy()
         a.destroy()
+
+
+def test_short_lists_direct_or_graph(pkg, monkeypatch):
+    """A two-command list (the paired float32 headline step) gives the same
+    bits issued as direct launches (the default below WGX_GRAPH_MIN) and
+    through a captured graph (WGX_GRAPH_MIN=0), on every replay, with the
+    input overwritten between replays so each replay must read it again."""
+    W, I = pkg.wgx, pkg.inputs
+    results = {}
+    for gmin in ("3", "0"):
+        monkeypatch.setenv("WGX_GRAPH_MIN", gmin)
+        ctx = W.Context(0)
+        try:
+            xa = ctx.from_numpy(I.uniform(61, (1, 16, 20, 20), -1, 1), "float32")
+            wa = ctx.from_numpy(I.uniform(62, (32, 16, 3, 3), -0.5, 0.5), "float32")
+            xb = ctx.from_numpy(I.uniform(63, (1, 32, 20, 20), -1, 1), "float32")
+            wb = ctx.from_numpy(I.uniform(64, (64, 32, 3, 3), -0.5, 0.5), "float32")
+            ya, yb = ctx.tensor("float32", [1, 32, 20, 20]), ctx.tensor("float32", [1, 64, 10, 10])
+            ctx.convolution(xa, wa, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 1, ya)
+            ctx.convolution(xb, wb, None, [2, 2], [1, 1], [1, 1], False, [0, 0], 1, yb)
+            outs = []
+            for rep in range(3):
+                xa.set_data(np.asarray(I.uniform(70 + rep, (1, 16, 20, 20), -1, 1), np.float32))
+                ctx.submit()
+                ctx.sync()
+                outs.append((ya.get_data().copy(), yb.get_data().copy()))
+            results[gmin] = outs
+        finally:
+            ctx.destroy()
+    for rep, ((a1, b1), (a2, b2)) in enumerate(zip(results["3"], results["0"])):
+        assert np.array_equal(a1.view(np.uint32), a2.view(np.uint32)), f"replay {rep}"
+        assert np.array_equal(b1.view(np.uint32), b2.view(np.uint32)), f"replay {rep}"
+    # each replay read the input written just before it
+    assert not np.array_equal(results["0"][0][0], results["0"][1][0])

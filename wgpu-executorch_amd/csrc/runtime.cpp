@@ -1271,12 +1271,8 @@ static int run_eager(wgx_ctx* c) { return issue_all(c); }
 // it replaces (the paired float32 headline step: 31.9 us per submit through
 // a graph, 26.8 us issued directly).  WGX_GRAPH_MIN=n moves the threshold.
 static size_t graph_min_cmds() {
-  static long v = -1;
-  if (v < 0) {
-    const char* e = getenv("WGX_GRAPH_MIN");
-    v = e ? std::max(0L, strtol(e, nullptr, 10)) : 3;
-  }
-  return (size_t)v;
+  const char* e = getenv("WGX_GRAPH_MIN");  // read per submit: a test may change it
+  return e ? (size_t)std::max(0L, strtol(e, nullptr, 10)) : 3;
 }
 
 int wgx_submit(wgx_ctx* c) {
