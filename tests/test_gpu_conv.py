@@ -581,7 +581,7 @@ CL_SEG_CASES = [
 
 
 @pytest.mark.parametrize("rv", ["1", "0"])
-@pytest.mark.parametrize("cfg", ["2x4w1", "2x2w1", "2x2w4", "1x2w8", "1x1w1"])
+@pytest.mark.parametrize("cfg", ["2x4w1", "2x2w1", "2x2w4", "2x1w4", "1x2w8", "1x1w1"])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_channel_last_row_segments(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg, rv):
     """The channel-last 16-bit kernel with its patch loaded as 16-byte row

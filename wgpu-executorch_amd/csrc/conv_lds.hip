@@ -999,9 +999,7 @@ template <bool CL, bool RV, int DT, int KH, int KW, int S>
 hipError_t launch_geo(const CParams& p, const Cfg& c, unsigned grid, hipStream_t s) {
   if (c.tm == 1 && c.tn == 1) return launch_cfg<CL, RV, DT, KH, KW, S, 1, 1>(p, c, grid, s);
   if (c.tm == 1 && c.tn == 2) return launch_cfg<CL, RV, DT, KH, KW, S, 1, 2>(p, c, grid, s);
-  // (the channel-last 64 x 32 tile with row segments would spill: not built)
-  if constexpr (!(CL && RV))
-    if (c.tm == 2 && c.tn == 1) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 1>(p, c, grid, s);
+  if (c.tm == 2 && c.tn == 1) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 1>(p, c, grid, s);
   if (c.tm == 2 && c.tn == 2) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 2>(p, c, grid, s);
   if constexpr (S == 1)
     if (c.tm == 2 && c.tn == 4) return launch_cfg<CL, RV, DT, KH, KW, S, 2, 4>(p, c, grid, s);
@@ -1199,12 +1197,13 @@ CParams make_params(const ConvLdsDesc& d, const Cfg& c) {
 // Images whose rows are whole 16-byte segments on a 16-byte base (float32: a
 // multiple of 4 columns, 16-bit: of 8) load the patch as row segments;
 // WGX_CONV_RV=0 keeps the element loads.
-// (the channel-last 64 x 32 tile takes row segments on pre-ordered weights
-// only: with the raw weights' registers it would spill)
-bool use_rv(const ConvLdsDesc& d, const Cfg& c, bool pre) {
+// (the channel-last 64 x 32 tile on raw weights spills 2 registers with row
+// segments and still gains: [1,128,80,80] -> 256 stride 2 12.7 -> 11.7 us,
+// [1,128,40,40] -> 256 12.0 -> 10.7)
+bool use_rv(const ConvLdsDesc& d, const Cfg& c) {
   const bool rv_off = getenv("WGX_CONV_RV") && strcmp(getenv("WGX_CONV_RV"), "0") == 0;
   return d.IW % (d.dtype == WGX_FLOAT32 ? 4 : 8) == 0 && (reinterpret_cast<uintptr_t>(d.x) & 15) == 0 &&
-         (d.dtype == WGX_FLOAT32 || (c.cl && (pre || !(c.tm == 2 && c.tn == 1)))) && !rv_off;
+         (d.dtype == WGX_FLOAT32 || c.cl) && !rv_off;
 }
 
 template <int SA, bool RVA, int SB, bool RVB>
@@ -1261,7 +1260,7 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   Cfg c = choose(d, cus);
   if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
   const bool pre = d.wpre && pre_form(c, d.sH);
-  c.rv = use_rv(d, c, pre);
+  c.rv = use_rv(d, c);
   CParams p = make_params(d, c);
   if (pre && c.rv && c.w == 1) {
     // the output-channel tiles of one pixel tile share its patch, in blocks
@@ -1309,8 +1308,8 @@ hipError_t launch_conv_lds_pair(const ConvLdsDesc& a, const ConvLdsDesc& b, int 
   // 4 waves per block for both (headline step, paired: 32 us at 4 waves,
   // 40 at 2, 55 at 1; 35.5 us as two launches)
   ca.w = cb.w = 4;
-  ca.rv = use_rv(a, ca, false);
-  cb.rv = use_rv(b, cb, false);
+  ca.rv = use_rv(a, ca);
+  cb.rv = use_rv(b, cb);
   const CParams pa = make_params(a, ca), pb = make_params(b, cb);
   if (pa.ntiles == 0 || pb.ntiles == 0 || (long long)pa.ntiles + pb.ntiles >= (1LL << 31)) return hipErrorNotSupported;
   if (is_dry(s)) return hipSuccess;
