@@ -202,8 +202,8 @@ __device__ __forceinline__ void conv_epilogue_t(const CParams& p, f32x16 (&acc)[
     // of output channel fr; v_permlane32_swap trades the upper half-wave's
     // row 2gp for the lower half-wave's row 2gp+1, so lane fr then holds all
     // 8 columns of row 2gp and lane fr + 32 all 8 of row 2gp + 1, and each
-    // lane writes one 16-byte run (half the store instructions, and half the
-    // separate runs the address unit takes, of 8-byte pieces)
+    // lane writes one 16-byte piece (half the store instructions of 8-byte
+    // pieces)
     const bool vec8 = (p.OW & 7) == 0 && ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 15) == 0;
     const bool vec4 = (p.OW & 3) == 0;
     auto store_rows = [&](int i, int j, int gp, const float4& a, const float4& b) {
