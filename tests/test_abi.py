@@ -134,9 +134,9 @@ def test_conv_validation_and_variants(hctx, pkg, monkeypatch):
     assert conv([1, 128, 80, 80], [256, 128, 3, 3], [1, 256, 40, 40], (2, 2), (1, 1), dtype="float32") == "conv_lds_f32_3x3s2_32x64w8"
     assert conv([1, 64, 80, 80], [128, 64, 3, 3], [1, 128, 80, 80], pad=(1, 1), dtype="bfloat16") == "conv_cl_bf16_3x3s1_32x64w4"
     assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1), dtype="float32") == "conv_lds_f32_3x3s1_64x64w1"
-    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1_pre"
-    assert conv([64, 64, 80, 80], [128, 64, 3, 3], [64, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1_pre"
-    assert conv([8, 32, 160, 160], [64, 32, 3, 3], [8, 64, 160, 160], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1_pre"
+    assert conv([16, 64, 80, 80], [128, 64, 3, 3], [16, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1c16_pre"
+    assert conv([64, 64, 80, 80], [128, 64, 3, 3], [64, 128, 80, 80], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1c16_pre"
+    assert conv([8, 32, 160, 160], [64, 32, 3, 3], [8, 64, 160, 160], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1c16_pre"
     assert conv([16, 128, 40, 40], [256, 128, 3, 3], [16, 256, 40, 40], pad=(1, 1)) == "conv_cl_f16_3x3s1_64x64w1_pre"
     assert conv([64, 128, 80, 80], [256, 128, 3, 3], [64, 256, 40, 40], (2, 2), (1, 1)) == "conv_cl_f16_3x3s2_64x64w1_pre"
     assert conv([2, 128, 40, 40], [256, 128, 3, 3], [2, 256, 40, 40], pad=(1, 1)) == "conv_cl_f16_3x3s1_32x64w8"

@@ -581,7 +581,7 @@ CL_SEG_CASES = [
 
 
 @pytest.mark.parametrize("rv", ["1", "0"])
-@pytest.mark.parametrize("cfg", ["2x4w1", "2x2w1", "2x2w4", "2x1w4", "1x2w8", "1x1w1"])
+@pytest.mark.parametrize("cfg", ["2x4w1", "2x2w1", "2x2w1c16", "2x2w4", "2x1w4", "1x2w8", "1x1w1"])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_channel_last_row_segments(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg, rv):
     """The channel-last 16-bit kernel with its patch loaded as 16-byte row
@@ -608,9 +608,11 @@ def test_channel_last_row_segments(gpu_ctx, orc, pkg, monkeypatch, dtype, cfg, r
                             activation=W.ACT_SILU if i % 2 else W.ACT_NONE)
         kernel = gpu_ctx.last_kernel
         tile = f"_{32 * int(cfg[0])}x{32 * int(cfg[2])}w{cfg.split('w')[1]}"
+        if rv == "0":
+            tile = tile.replace("c16", "")  # 16-column regions take row segments only
         # the one-wave 64 x 64 tile (either stride) and 64 x 128 tile (stride
         # 1) run on pre-ordered weights (a reorder pass first)
-        pre = cfg in ("2x4w1", "2x2w1")
+        pre = cfg in ("2x4w1", "2x2w1", "2x2w1c16")
         assert kernel.startswith("conv_cl_") and kernel.endswith(tile + ("_pre" if pre else "")), kernel
         gpu_ctx.submit()
         gpu_ctx.sync()
@@ -631,9 +633,11 @@ def test_batched_16bit_convolution_default_choice(gpu_ctx, orc, pkg, monkeypatch
     output element against the float64 convolution."""
     I = pkg.inputs
     monkeypatch.setenv("WGX_CONV_PRE", pre)
+    # (16-column regions at stride 1 where the width is a multiple of 16)
+    want16 = "conv_cl_f16_3x3s1_64x64w1c16_pre" if pre == "1" else "conv_cl_f16_3x3s1_64x128w1"
     want = "conv_cl_f16_3x3s1_64x64w1_pre" if pre == "1" else "conv_cl_f16_3x3s1_64x128w1"
     want2 = "conv_cl_f16_3x3s2_64x64w1_pre" if pre == "1" else "gemm_mfma_f16"
-    cases = [((128, 32, 32, 32), (64, 32, 3, 3), 1, 1, want), ((256, 32, 20, 24), (40, 32, 3, 3), 1, 1, want),
+    cases = [((128, 32, 32, 32), (64, 32, 3, 3), 1, 1, want16), ((256, 32, 20, 24), (40, 32, 3, 3), 1, 1, want),
              ((512, 32, 20, 24), (40, 32, 3, 3), 2, 1, want2)]
     for i, (xs, ws, s, p, want) in enumerate(cases):
         x = round_in(I.uniform(2900 + i, xs, -1, 1), "float16")
@@ -718,6 +722,8 @@ CLAMP_RES_CASES = [
     ((2, 32, 16, 16), (256, 32, 3, 3), 1, 1, 1, "2x2w1"),
     ((2, 32, 18, 16), (128, 32, 3, 3), 2, 1, 1, "2x2w1"),
     ((1, 32, 17, 13), (24, 32, 3, 3), 1, 1, 1, "2x2w4"),
+    ((2, 32, 16, 24), (128, 32, 3, 3), 1, 1, 1, "2x2w1c16"),   # 16-column regions, ragged last
+    ((1, 32, 22, 40), (256, 32, 3, 3), 2, 1, 1, "2x2w1c16"),   # the same at stride 2
     ((2, 48, 20, 20), (48, 1, 3, 3), 1, 1, 48, None),
     ((2, 64, 20, 20), (64, 1, 5, 5), 2, 2, 64, None),
 ]
@@ -746,8 +752,8 @@ def test_conv_clamp_and_residual(gpu_ctx, orc, pkg, monkeypatch, dtype):
         gpu_ctx.convolution(tx, tw, tb, [s, s], [p, p], [1, 1], False, [0, 0], g, ty, clamp=(lo, hi),
                             activation=W.ACT_SILU, residual=tr, conv_scale=cs, residual_scale=rs)
         kernel = gpu_ctx.last_kernel
-        if cfg == "2x2w1" and dtype != "float32":
-            assert kernel.endswith("_pre"), kernel
+        if cfg in ("2x2w1", "2x2w1c16") and dtype != "float32":
+            assert kernel.endswith(("c16_pre" if cfg.endswith("c16") else "w1_pre")), kernel
         gpu_ctx.submit()
         gpu_ctx.sync()
         want = cs * np.clip(ref / (1.0 + np.exp(-ref)), lo, hi) + rs * r.astype(np.float64)

@@ -177,7 +177,7 @@ struct Geo {
 // activation and clamp, one rounding, 8- or 16-byte stores.
 // CL / RS: the launch clamps / adds a residual (one instantiation each, so
 // the per-element code carries no selects for what the launch does not do).
-template <int DT, int TM, int TN, bool CL, bool RS>
+template <int DT, int TM, int TN, bool CL, bool RS, int CW>
 __device__ __forceinline__ void conv_epilogue_t(const CParams& p, f32x16 (&acc)[TM][TN], char* lds, int W, int wave,
                                                 int lane, int m0, int oh0, int ow0, int z, const float (&brow)[TM]) {
   constexpr int ES = DT == WGX_FLOAT32 ? 4 : 2;
@@ -197,13 +197,15 @@ __device__ __forceinline__ void conv_epilogue_t(const CParams& p, f32x16 (&acc)[
     __syncthreads();
   }
   char* yimg = static_cast<char*>(p.y) + (long long)z * p.sy * ES;
+  static_assert(ES == 2 || CW == 8, "float32 regions are 8 columns wide");
   if constexpr (ES == 2) {
-    // 16-bit: lane (fr, fc) holds columns 4fc..4fc+3 of rows 2gp and 2gp+1
-    // of output channel fr; v_permlane32_swap trades the upper half-wave's
-    // row 2gp for the lower half-wave's row 2gp+1, so lane fr then holds all
-    // 8 columns of row 2gp and lane fr + 32 all 8 of row 2gp + 1, and each
-    // lane writes one 16-byte piece (half the store instructions of 8-byte
-    // pieces)
+    // 16-bit: lane (fr, fc) holds pixels 8g + 4fc .. 8g + 4fc + 3 of the
+    // 32-pixel block (groups g = 2gp and 2gp + 1) of output channel fr;
+    // v_permlane32_swap trades the upper half-wave's group 2gp for the lower
+    // half-wave's group 2gp + 1, so lane fr then holds all 8 pixels of group
+    // 2gp and lane fr + 32 those of group 2gp + 1, and each lane writes one
+    // 16-byte piece (CW = 8: rows 2gp and 2gp + 1; CW = 16: the two halves of
+    // one 32-byte row, which the address unit merges)
     const bool vec8 = (p.OW & 7) == 0 && ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 15) == 0;
     const bool vec4 = (p.OW & 3) == 0;
     auto store_rows = [&](int i, int j, int gp, const float4& a, const float4& b) {
@@ -215,15 +217,17 @@ __device__ __forceinline__ void conv_epilogue_t(const CParams& p, f32x16 (&acc)[
         v[d] = __uint_as_float(r[0]);
         v[4 + d] = __uint_as_float(r[1]);
       }
-      const int oc = m0 + i * 32 + fr, oh = oh0 + 4 * j + 2 * gp + fc;
-      if (oc >= p.OC || oh >= p.OH || ow0 >= p.OW) return;
+      constexpr int RB = 32 / CW;
+      const int px = 8 * (2 * gp + fc);  // the group's first pixel in the block
+      const int oc = m0 + i * 32 + fr, oh = oh0 + RB * j + px / CW, ow = ow0 + px % CW;
+      if (oc >= p.OC || oh >= p.OH || ow >= p.OW) return;
       float bias = 0.0f;
 #pragma unroll
       for (int ii = 0; ii < TM; ++ii)
         if (ii == i) bias = brow[ii];
-      const long long eo = (long long)oc * p.OH * p.OW + (long long)oh * p.OW + ow0;
+      const long long eo = (long long)oc * p.OH * p.OW + (long long)oh * p.OW + ow;
       uint16_t* dst = reinterpret_cast<uint16_t*>(yimg) + eo;
-      const bool full = ow0 + 7 < p.OW;
+      const bool full = ow + 7 < p.OW;
       // the residual's elements at the output's positions, read by the lane
       // that writes them (a residual that is the output itself is fine)
       uint32_t rr[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
@@ -237,7 +241,7 @@ __device__ __forceinline__ void conv_epilogue_t(const CParams& p, f32x16 (&acc)[
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            if (ow0 + e < p.OW) rr[e] = rp[e];
+            if (ow + e < p.OW) rr[e] = rp[e];
         }
       }
       uint32_t h[8];
@@ -252,11 +256,11 @@ __device__ __forceinline__ void conv_epilogue_t(const CParams& p, f32x16 (&acc)[
         *reinterpret_cast<uint4*>(dst) = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
       } else if (vec4) {
         *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-        if (ow0 + 4 < p.OW) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+        if (ow + 4 < p.OW) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(h[4] | (h[5] << 16), h[6] | (h[7] << 16));
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (ow0 + e < p.OW) dst[e] = (uint16_t)h[e];
+          if (ow + e < p.OW) dst[e] = (uint16_t)h[e];
       }
     };
     auto grp = [&](const f32x16& x, int g) { return make_float4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]); };
@@ -363,15 +367,15 @@ __device__ __forceinline__ void conv_epilogue_t(const CParams& p, f32x16 (&acc)[
   }
 }
 
-template <int DT, int TM, int TN>
+template <int DT, int TM, int TN, int CW = 8>
 __device__ __forceinline__ void conv_epilogue(const CParams& p, f32x16 (&acc)[TM][TN], char* lds, int W, int wave,
                                               int lane, int m0, int oh0, int ow0, int z, const float (&brow)[TM]) {
   if (p.has_clamp) {
-    if (p.res) conv_epilogue_t<DT, TM, TN, true, true>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
-    else conv_epilogue_t<DT, TM, TN, true, false>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+    if (p.res) conv_epilogue_t<DT, TM, TN, true, true, CW>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+    else conv_epilogue_t<DT, TM, TN, true, false, CW>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
   } else {
-    if (p.res) conv_epilogue_t<DT, TM, TN, false, true>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
-    else conv_epilogue_t<DT, TM, TN, false, false>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+    if (p.res) conv_epilogue_t<DT, TM, TN, false, true, CW>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+    else conv_epilogue_t<DT, TM, TN, false, false, CW>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
   }
 }
 
@@ -647,10 +651,13 @@ __global__ __launch_bounds__(256) void k_conv_lds_pair(CParams pa, CParams pb, i
 // then the odd ones), 32 bytes a slot.  The 16-byte stagger between the rows
 // that consecutive 8-lane groups read and the column split at stride 2 put
 // the 16 lanes of one LDS cycle on different banks.
-template <int KH, int KW, int S, int TN>
+// CW: output columns of the region, 8 (32-pixel blocks of 4 rows x 8) or 16
+// (blocks of 2 rows x 16: longer patch rows and 32-byte output row pieces)
+template <int KH, int KW, int S, int TN, int CW = 8>
 struct GeoCL {
   static constexpr int T = KH * KW;
-  static constexpr int RH = 4 * TN, RW = 8;
+  static constexpr int RB = 32 / CW;  // rows of a 32-pixel block
+  static constexpr int RH = RB * TN, RW = CW;
   static constexpr int PH = (RH - 1) * S + KH, PW = (RW - 1) * S + KW;
   static constexpr int PHW = PH * PW;
   static constexpr int NBLK = (PHW + 63) / 64;  // patch pixels per lane
@@ -679,10 +686,10 @@ struct GeoCL {
 // rows are contiguous; they stream RING taps
 // ahead of the multiplies instead of a whole chunk ahead, which frees the
 // registers of the chunk-ahead copy and its rebuild.
-template <int DT, int KH, int KW, int S, int TM, int TN, bool RV, bool PRE = false>
+template <int DT, int KH, int KW, int S, int TM, int TN, bool RV, bool PRE = false, int CW = 8>
 __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512)
 __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl(CParams p) {
-  using G = GeoCL<KH, KW, S, TN>;
+  using G = GeoCL<KH, KW, S, TN, CW>;
   constexpr int T = G::T, NBLK = G::NBLK;
   constexpr int RING = 3;
   // the next chunk's tap t + RING - T takes the slot tap t just left
@@ -780,10 +787,10 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
     const int oc = m0 + i * 32 + fr;
     brow[i] = (p.bias && oc < p.OC) ? to_f<DT>((uint32_t)reinterpret_cast<const uint16_t*>(p.bias)[oc]) : 0.0f;
   }
-  // B: the lane's output pixel (row 4j + fr/8, column fr%8 of the region)
+  // B: the lane's output pixel (row RB*j + fr/CW, column fr%CW of the region)
   int vb[TN];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) vb[j] = G::row((4 * j + (fr >> 3)) * S) + (fr & 7) * 32 + fc * 16;
+  for (int j = 0; j < TN; ++j) vb[j] = G::row((G::RB * j + fr / CW) * S) + (fr % CW) * 32 + fc * 16;
 
   const char* ximg = static_cast<const char*>(p.x) + (long long)z * p.sx * 2;
   const char* wbase = static_cast<const char*>(p.w);
@@ -938,7 +945,7 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
     asm volatile("" ::: "memory");
   }
 
-  conv_epilogue<DT, TM, TN>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
+  conv_epilogue<DT, TM, TN, CW>(p, acc, lds, W, wave, lane, m0, oh0, ow0, z, brow);
 }
 
 // 16-bit weights [OC][IC][T] -> [IC/16][T][OC][16]: for chunk q and tap t
@@ -961,6 +968,7 @@ struct Cfg {
   int tm, tn, w;
   bool cl;  // 16-bit data: the channel-last kernel (else the channel-major one)
   bool rv;  // float32: the patch loaded as 16-byte row segments
+  int cw = 8;  // output columns of a region (16: the channel-last tile on pre-ordered weights)
 };
 
 template <bool CL, bool RV, int DT, int KH, int KW, int S, int TM, int TN>
@@ -1022,23 +1030,23 @@ hipError_t launch_dt(const CParams& p, const Cfg& c, int S, unsigned grid, hipSt
 
 // LDS bytes of a channel-last block of W waves: their patches, or the
 // partial sums of their reduction, whichever is larger.
-template <int S, int TM, int TN>
+template <int S, int TM, int TN, int CW = 8>
 size_t cl_block_lds(int W) {
-  const size_t patch = (size_t)W * GeoCL<3, 3, S, TN>::LDS_WAVE;
+  const size_t patch = (size_t)W * GeoCL<3, 3, S, TN, CW>::LDS_WAVE;
   const size_t part = W > 1 ? (size_t)W * TM * TN * 4 * 64 * 16 : 0;
   return patch > part ? patch : part;
 }
 
 // The channel-last tile on pre-ordered weights: the reorder pass into wpre,
 // then the kernel reading them, in blocks of W waves.
-template <int DT, bool RV, int TM, int TN, int S>
+template <int DT, bool RV, int TM, int TN, int S, int CW = 8>
 hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned grid, int W, hipStream_t s) {
   // a shared patch: two buffers for the block (W is 1 then)
-  const size_t lds = p.share > 1 ? 2 * (size_t)GeoCL<3, 3, S, TN>::LDS_WAVE : cl_block_lds<S, TM, TN>(W);
+  const size_t lds = p.share > 1 ? 2 * (size_t)GeoCL<3, 3, S, TN, CW>::LDS_WAVE : cl_block_lds<S, TM, TN, CW>(W);
   const int nw = p.share > 1 ? p.share : W;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   if (is_dry(s)) return hipSuccess;
-  auto fn = k_conv_cl<DT, 3, 3, S, TM, TN, RV, true>;
+  auto fn = k_conv_cl<DT, 3, 3, S, TM, TN, RV, true, CW>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -1072,6 +1080,11 @@ bool pre_form(const Cfg& c, int S) {
 template <int DT>
 hipError_t launch_pre_dt(const CParams& p, const Cfg& c, int S, const void* w, void* wpre, unsigned grid,
                          hipStream_t s) {
+  if (c.cw == 16) {  // row segments only (the caller keeps 8 columns otherwise)
+    if (c.tm == 2 && c.tn == 2 && S == 2) return launch_cl_pre<DT, true, 2, 2, 2, 16>(p, w, wpre, grid, c.w, s);
+    if (c.tm == 2 && c.tn == 2 && S == 1) return launch_cl_pre<DT, true, 2, 2, 1, 16>(p, w, wpre, grid, c.w, s);
+    return hipErrorInvalidValue;
+  }
   if (c.tm == 2 && c.tn == 2 && S == 2)
     return c.rv ? launch_cl_pre<DT, true, 2, 2, 2>(p, w, wpre, grid, c.w, s)
                 : launch_cl_pre<DT, false, 2, 2, 2>(p, w, wpre, grid, c.w, s);
@@ -1089,8 +1102,9 @@ hipError_t launch_pre_dt(const CParams& p, const Cfg& c, int S, const void* w, v
 int chunk_channels(int dtype) { return dtype == WGX_FLOAT32 ? 8 : 16; }
 
 long long tile_count(const ConvLdsDesc& d, const Cfg& c) {
-  return (long long)d.B * ((d.OC + 32 * c.tm - 1) / (32 * c.tm)) * ((d.OH + 4 * c.tn - 1) / (4 * c.tn)) *
-         ((d.OW + 7) / 8);
+  const int rh = 32 / c.cw * c.tn;  // output rows of a region
+  return (long long)d.B * ((d.OC + 32 * c.tm - 1) / (32 * c.tm)) * ((d.OH + rh - 1) / rh) *
+         ((d.OW + c.cw - 1) / c.cw);
 }
 
 // The configuration for a shape, from sweeps of the 3x3 maps [1,64,80,80] ->
@@ -1128,6 +1142,12 @@ Cfg choose(const ConvLdsDesc& d, int cus) {
     if (pre) {
       // the 64 x 64 tile, at either stride, while it gives every SIMD a wave
       m.tn = 2;
+      // 16-column regions at stride 1 on widths that fill them (WGX_CONV_CW=8
+      // keeps 8): [64,64,80,80] -> 128 123.8 -> 110.7 us, [8,32,160,160] -> 64
+      // 30.6 -> 28.1; at stride 2 they tie (129.5 / 129.6 us), at width 40
+      // they lose a little (33.1 -> 33.6: a third of the last region empty)
+      const bool cw8 = getenv("WGX_CONV_CW") && strcmp(getenv("WGX_CONV_CW"), "8") == 0;
+      if (d.sH == 1 && d.OW % 16 == 0 && !cw8) m.cw = 16;
       if (!(seg && tile_count(d, m) >= simds)) m.tm = 0;
     } else if (!(seg && d.sH == 1 && tile_count(d, m) >= simds)) {
       m.tm = 0;
@@ -1153,9 +1173,14 @@ Cfg choose(const ConvLdsDesc& d, int cus) {
     c = many16();
   }
   if (const char* e = getenv("WGX_CONV_LDS")) {
-    int tm = 0, tn = 0, ww = 0;
-    if (sscanf(e, "%dx%dw%d", &tm, &tn, &ww) == 3 && tm >= 1 && tm <= 2 && tn >= 1 && tn <= 4 && ww >= 1 && ww <= 8)
+    // TMxTNwW, or TMxTNwWc16 for 16-column regions (kept on the pre-ordered
+    // 64 x 64 tile only)
+    int tm = 0, tn = 0, ww = 0, cwv = 8;
+    if (sscanf(e, "%dx%dw%dc%d", &tm, &tn, &ww, &cwv) >= 3 && tm >= 1 && tm <= 2 && tn >= 1 && tn <= 4 && ww >= 1 &&
+        ww <= 8) {
       c = Cfg{tm, tn, ww, cl};
+      c.cw = cwv == 16 ? 16 : 8;
+    }
   }
   return c;
 }
@@ -1178,8 +1203,8 @@ CParams make_params(const ConvLdsDesc& d, const Cfg& c) {
   p.sx = (long long)d.IC * d.IH * d.IW;
   p.sy = (long long)d.OC * d.OH * d.OW;
   p.tiles_m = (d.OC + 32 * c.tm - 1) / (32 * c.tm);
-  p.tiles_h = (d.OH + 4 * c.tn - 1) / (4 * c.tn);
-  p.tiles_w = (d.OW + 7) / 8;
+  p.tiles_h = (d.OH + 32 / c.cw * c.tn - 1) / (32 / c.cw * c.tn);
+  p.tiles_w = (d.OW + c.cw - 1) / c.cw;
   p.ntiles = d.B * p.tiles_m * p.tiles_h * p.tiles_w;
   p.share = 1;
   p.nchunks = d.IC / chunk_channels(d.dtype);
@@ -1261,6 +1286,7 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   if (c.tm == 0) return hipErrorInvalidValue;  // the caller takes another kernel
   const bool pre = d.wpre && pre_form(c, d.sH);
   c.rv = use_rv(d, c);
+  if (!(pre && c.rv && c.tm == 2 && c.tn == 2)) c.cw = 8;
   CParams p = make_params(d, c);
   if (pre && c.rv && c.w == 1) {
     // the output-channel tiles of one pixel tile share its patch, in blocks
@@ -1277,9 +1303,9 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
   }
   if (name) {
     char buf[96];
-    snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d%s", c.cl ? "cl" : "lds",
+    snprintf(buf, sizeof buf, "conv_%s_%s_%dx%ds%d_%dx%dw%d%s%s", c.cl ? "cl" : "lds",
              d.dtype == WGX_FLOAT32 ? "f32" : (d.dtype == WGX_BFLOAT16 ? "bf16" : "f16"), d.KH, d.KW, d.sH,
-             32 * c.tm, 32 * c.tn, c.w, pre ? "_pre" : "");
+             32 * c.tm, 32 * c.tn, c.w, c.cw == 16 ? "c16" : "", pre ? "_pre" : "");
     *name = buf;
   }
   if (p.ntiles == 0) return hipSuccess;
