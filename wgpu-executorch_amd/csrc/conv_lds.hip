@@ -686,7 +686,7 @@ struct GeoCL {
 // rows are contiguous; they stream RING taps
 // ahead of the multiplies instead of a whole chunk ahead, which frees the
 // registers of the chunk-ahead copy and its rebuild.
-template <int DT, int KH, int KW, int S, int TM, int TN, bool RV, bool PRE = false, int CW = 8>
+template <int DT, int KH, int KW, int S, int TM, int TN, bool RV, bool PRE = false, int CW = 8, bool SH = false>
 __global__ __launch_bounds__(TM * TN >= 4 ? 256 : 512)
 __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl(CParams p) {
   using G = GeoCL<KH, KW, S, TN, CW>;
@@ -705,7 +705,9 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   // SHW > 1 (pre-ordered weights, row segments, W = 1): the block's waves take
   // output-channel tiles tmb*SHW + wave of one pixel tile and load one shared
   // patch between them, each wave a contiguous share of its segment tasks
-  const int SHW = (PRE && RV) ? p.share : 1;
+  // (SH: built for a shared patch, p.share >= 2, so a wave's share of the
+  // segment tasks fits fewer passes)
+  const int SHW = (PRE && RV && SH) ? p.share : 1;
   const int sw = SHW > 1 ? wave : 0;
   // XCD-aware numbering, output-channel tiles fastest (as in k_conv_lds)
   const int Gn = gridDim.x;
@@ -757,7 +759,7 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   // pair each).  sp: its input offset in channel 0 of the chunk (OOB
   // outside), sr: LDS offset of its row and channel half (-1: no task), sg:
   // the patch column of its first pixel
-  constexpr int NS = RV ? G::NPASS : 1;
+  constexpr int NS = RV ? (SH ? ((G::NTASK + 1) / 2 + 63) / 64 : G::NPASS) : 1;
   uint32_t sp[NS];
   int sr[NS], sg[NS];
   // tasks per wave: all of them, or a contiguous share of a shared patch
@@ -765,7 +767,7 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
   if constexpr (RV) {
     const int a0 = iw0 - (((iw0 % 8) + 8) % 8), dl = iw0 - a0;
 #pragma unroll
-    for (int e = 0; e < G::NPASS; ++e) {
+    for (int e = 0; e < NS; ++e) {
       const int ql = e * 64 + lane, q = sw * qpw + ql, rh = q / G::NSEG, g = q - rh * G::NSEG;
       const int h = rh & 1, r = rh >> 1;
       const int ih = ih0 + r, s0 = a0 + 8 * g;
@@ -814,7 +816,7 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
     const rsrc_t rx = rsrc(ximg + (long long)c * chunk_x, chunk_x);
     if constexpr (RV) {
 #pragma unroll
-      for (int e = 0; e < G::NPASS; ++e)
+      for (int e = 0; e < NS; ++e)
         if (e * 64 < qpw) {
 #pragma unroll
           for (int ch = 0; ch < 8; ++ch) ps[e][ch] = ld16(rx, sp[e], ch * cplane);
@@ -833,7 +835,7 @@ __attribute__((amdgpu_waves_per_eu(PRE && TM * TN == 4 ? 2 : 1))) void k_conv_cl
     if constexpr (RV) {
       auto dw = [](const uint4& v, int d) { return d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w; };
 #pragma unroll
-      for (int e = 0; e < G::NPASS; ++e)
+      for (int e = 0; e < NS; ++e)
         if (sr[e] >= 0) {
 #pragma unroll
           for (int px = 0; px < 8; ++px) {
@@ -1039,14 +1041,14 @@ size_t cl_block_lds(int W) {
 
 // The channel-last tile on pre-ordered weights: the reorder pass into wpre,
 // then the kernel reading them, in blocks of W waves.
-template <int DT, bool RV, int TM, int TN, int S, int CW = 8>
+template <int DT, bool RV, int TM, int TN, int S, int CW = 8, bool SH = false>
 hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned grid, int W, hipStream_t s) {
   // a shared patch: two buffers for the block (W is 1 then)
   const size_t lds = p.share > 1 ? 2 * (size_t)GeoCL<3, 3, S, TN, CW>::LDS_WAVE : cl_block_lds<S, TM, TN, CW>(W);
   const int nw = p.share > 1 ? p.share : W;
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   if (is_dry(s)) return hipSuccess;
-  auto fn = k_conv_cl<DT, 3, 3, S, TM, TN, RV, true, CW>;
+  auto fn = k_conv_cl<DT, 3, 3, S, TM, TN, RV, true, CW, SH>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -1066,6 +1068,15 @@ hipError_t launch_cl_pre(const CParams& p, const void* w, void* wpre, unsigned g
   return hipGetLastError();
 }
 
+// A shared patch (p.share >= 2, row segments only) takes the kernel built
+// for it: a wave's share of the segment tasks fits fewer passes.
+template <int DT, bool RV, int TM, int TN, int S, int CW = 8>
+hipError_t launch_cl_pre_sh(const CParams& p, const void* w, void* wpre, unsigned grid, int W, hipStream_t s) {
+  if constexpr (RV)
+    if (p.share > 1) return launch_cl_pre<DT, RV, TM, TN, S, CW, true>(p, w, wpre, grid, W, s);
+  return launch_cl_pre<DT, RV, TM, TN, S, CW, false>(p, w, wpre, grid, W, s);
+}
+
 // The tiles that run on pre-ordered weights: 64 x 64 one-wave (either
 // stride) and 64 x 128 one-wave (stride 1).  The batch-1 split-chunk tiles
 // keep the raw weights: on them the kernel gains (32 x 64 s1 [1,64,80,80]
@@ -1081,19 +1092,19 @@ template <int DT>
 hipError_t launch_pre_dt(const CParams& p, const Cfg& c, int S, const void* w, void* wpre, unsigned grid,
                          hipStream_t s) {
   if (c.cw == 16) {  // row segments only (the caller keeps 8 columns otherwise)
-    if (c.tm == 2 && c.tn == 2 && S == 2) return launch_cl_pre<DT, true, 2, 2, 2, 16>(p, w, wpre, grid, c.w, s);
-    if (c.tm == 2 && c.tn == 2 && S == 1) return launch_cl_pre<DT, true, 2, 2, 1, 16>(p, w, wpre, grid, c.w, s);
+    if (c.tm == 2 && c.tn == 2 && S == 2) return launch_cl_pre_sh<DT, true, 2, 2, 2, 16>(p, w, wpre, grid, c.w, s);
+    if (c.tm == 2 && c.tn == 2 && S == 1) return launch_cl_pre_sh<DT, true, 2, 2, 1, 16>(p, w, wpre, grid, c.w, s);
     return hipErrorInvalidValue;
   }
   if (c.tm == 2 && c.tn == 2 && S == 2)
-    return c.rv ? launch_cl_pre<DT, true, 2, 2, 2>(p, w, wpre, grid, c.w, s)
-                : launch_cl_pre<DT, false, 2, 2, 2>(p, w, wpre, grid, c.w, s);
+    return c.rv ? launch_cl_pre_sh<DT, true, 2, 2, 2>(p, w, wpre, grid, c.w, s)
+                : launch_cl_pre_sh<DT, false, 2, 2, 2>(p, w, wpre, grid, c.w, s);
   if (c.tm == 2 && c.tn == 2)
-    return c.rv ? launch_cl_pre<DT, true, 2, 2, 1>(p, w, wpre, grid, c.w, s)
-                : launch_cl_pre<DT, false, 2, 2, 1>(p, w, wpre, grid, c.w, s);
+    return c.rv ? launch_cl_pre_sh<DT, true, 2, 2, 1>(p, w, wpre, grid, c.w, s)
+                : launch_cl_pre_sh<DT, false, 2, 2, 1>(p, w, wpre, grid, c.w, s);
   if (c.tm == 2 && c.tn == 4 && S == 1)
-    return c.rv ? launch_cl_pre<DT, true, 2, 4, 1>(p, w, wpre, grid, c.w, s)
-                : launch_cl_pre<DT, false, 2, 4, 1>(p, w, wpre, grid, c.w, s);
+    return c.rv ? launch_cl_pre_sh<DT, true, 2, 4, 1>(p, w, wpre, grid, c.w, s)
+                : launch_cl_pre_sh<DT, false, 2, 4, 1>(p, w, wpre, grid, c.w, s);
   return hipErrorInvalidValue;
 }
 
