@@ -162,12 +162,18 @@ struct Geo {
   // A fragments kept in flight ahead of the one being multiplied
   static constexpr int PF = ES == 4 ? STEPS / 3 : STEPS;
   static_assert(STEPS % PF == 0, "the prefetch ring wraps at chunk ends");
-  // LDS byte offset, relative to the lane's pixel base, of element e of
-  // fragment step s (lane half channel = k / T, tap = k % T, k = s*EPC + e)
-  static constexpr int boff(int s, int e) {
-    const int k = s * EPC + e, ch = k / T, tap = k % T;
+  // Interleaved lane halves (the weight loads): element e of fragment s in
+  // lane half h is chunk k = 2*EPC*s + EPC*h + e (channel k / T, tap k % T),
+  // so the two halves of a fragment are neighbouring 16-byte pieces of one
+  // weight row, which the address unit takes as one run.  koff(k): LDS byte
+  // offset of chunk k from the lane's pixel base; the upper half adds
+  // dhalf(t) to the lower half's koff for a lower-half tap t (the same for
+  // every channel).
+  static constexpr int koff(int k) {
+    const int ch = k / T, tap = k % T;
     return (ch * PHWP + (tap / KW) * ROWP + (tap % KW)) * ES;
   }
+  static constexpr int dhalf(int t) { return koff(t + EPC) - koff(t); }
 };
 
 // Epilogue shared by the convolution kernels: acc[i][j][4g + e] is output
@@ -414,7 +420,7 @@ __device__ __forceinline__ void conv_lds_tile(const CParams& p, int blk, int nbl
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int oc = m0 + i * 32 + fr;
-    va[i] = oc < p.OC ? (uint32_t)(oc * K + fc * G::CPL * T) * ES : OOB;
+    va[i] = oc < p.OC ? (uint32_t)(oc * K * ES + fc * 16) : OOB;
   }
   // patch block e of a channel: this lane's (row, column) of the patch
   // and its input offset in channel 0 of the chunk (OOB outside the image or
@@ -457,10 +463,15 @@ __device__ __forceinline__ void conv_lds_tile(const CParams& p, int blk, int nbl
                                      : (uint32_t)reinterpret_cast<const uint16_t*>(p.bias)[oc])
                   : 0.0f;
   }
-  int vb[TN];
+  // per region block j and lower-half tap t: the lane's B base (its pixel,
+  // plus what the upper lane half adds for that tap; see Geo::koff)
+  int vb[TN][T];
 #pragma unroll
-  for (int j = 0; j < TN; ++j)
-    vb[j] = (fc * G::CPL * G::PHWP + ((4 * j + (fr >> 3)) * S) * G::ROWP + (fr & 7) * S + dl) * ES;
+  for (int j = 0; j < TN; ++j) {
+    const int v0 = (((4 * j + (fr >> 3)) * S) * G::ROWP + (fr & 7) * S + dl) * ES;
+#pragma unroll
+    for (int t = 0; t < T; ++t) vb[j][t] = v0 + (fc ? G::dhalf(t) : 0);
+  }
 
   const char* ximg = static_cast<const char*>(p.x) + (long long)z * p.sx * ES;
   const char* wbase = static_cast<const char*>(p.w);
@@ -536,7 +547,7 @@ __device__ __forceinline__ void conv_lds_tile(const CParams& p, int blk, int nbl
 #pragma unroll
     for (int s = 0; s < PF; ++s)
 #pragma unroll
-      for (int i = 0; i < TM; ++i) a[s][i] = ld16(rw0, va[i], (uint32_t)(s * 16));
+      for (int i = 0; i < TM; ++i) a[s][i] = ld16(rw0, va[i], (uint32_t)(s * 32));
   }
   for (; c < p.nchunks; c += W) {
     const bool more = c + W < p.nchunks;
@@ -551,23 +562,28 @@ __device__ __forceinline__ void conv_lds_tile(const CParams& p, int blk, int nbl
     // (two register sets; the scheduling barriers keep the compiler from
     // sinking the reads next to their first use)
     auto read_b = [&](uint4* bf, int s) {
+      // element e of fragment s: chunk k = 2*EPC*s + e (lower half; the
+      // upper half's k + EPC through the lane's base for tap k % T)
+      auto ld = [&](int j, int e) -> const char* {
+        const int k = 2 * G::EPC * s + e;
+        return wl + vb[j][k % T] + G::koff(k);
+      };
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const char* pb = wl + vb[j];
         if constexpr (ES == 4) {
-          bf[j].x = *reinterpret_cast<const uint32_t*>(pb + G::boff(s, 0));
-          bf[j].y = *reinterpret_cast<const uint32_t*>(pb + G::boff(s, 1));
-          bf[j].z = *reinterpret_cast<const uint32_t*>(pb + G::boff(s, 2));
-          bf[j].w = *reinterpret_cast<const uint32_t*>(pb + G::boff(s, 3));
+          bf[j].x = *reinterpret_cast<const uint32_t*>(ld(j, 0));
+          bf[j].y = *reinterpret_cast<const uint32_t*>(ld(j, 1));
+          bf[j].z = *reinterpret_cast<const uint32_t*>(ld(j, 2));
+          bf[j].w = *reinterpret_cast<const uint32_t*>(ld(j, 3));
         } else {
-          const uint32_t h0 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 0));
-          const uint32_t h1 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 1));
-          const uint32_t h2 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 2));
-          const uint32_t h3 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 3));
-          const uint32_t h4 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 4));
-          const uint32_t h5 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 5));
-          const uint32_t h6 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 6));
-          const uint32_t h7 = *reinterpret_cast<const uint16_t*>(pb + G::boff(s, 7));
+          const uint32_t h0 = *reinterpret_cast<const uint16_t*>(ld(j, 0));
+          const uint32_t h1 = *reinterpret_cast<const uint16_t*>(ld(j, 1));
+          const uint32_t h2 = *reinterpret_cast<const uint16_t*>(ld(j, 2));
+          const uint32_t h3 = *reinterpret_cast<const uint16_t*>(ld(j, 3));
+          const uint32_t h4 = *reinterpret_cast<const uint16_t*>(ld(j, 4));
+          const uint32_t h5 = *reinterpret_cast<const uint16_t*>(ld(j, 5));
+          const uint32_t h6 = *reinterpret_cast<const uint16_t*>(ld(j, 6));
+          const uint32_t h7 = *reinterpret_cast<const uint16_t*>(ld(j, 7));
           bf[j] = make_uint4(h0 | (h1 << 16), h2 | (h3 << 16), h4 | (h5 << 16), h6 | (h7 << 16));
         }
       }
@@ -581,10 +597,10 @@ __device__ __forceinline__ void conv_lds_tile(const CParams& p, int blk, int nbl
       for (int i = 0; i < TM; ++i) af[i] = a[s % PF][i];
       if (s + PF < STEPS) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[s % PF][i] = ld16(rw, va[i], (uint32_t)((s + PF) * 16));
+        for (int i = 0; i < TM; ++i) a[s % PF][i] = ld16(rw, va[i], (uint32_t)((s + PF) * 32));
       } else if (more) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[s % PF][i] = ld16(rn, va[i], (uint32_t)((s + PF - STEPS) * 16));
+        for (int i = 0; i < TM; ++i) a[s % PF][i] = ld16(rn, va[i], (uint32_t)((s + PF - STEPS) * 32));
       }
       if (s + 1 < STEPS) read_b(bb[(s + 1) & 1], s + 1);
       __builtin_amdgcn_sched_barrier(0);
