@@ -628,7 +628,9 @@ def main():
         _, _, per_kernel["pair"] = measure(W, build_pair, int(300e6 / pair_bytes) + 1, reps_shape=5, reps_amort=10,
                                            graph=False)
         dom, flops_dom, bytes_dom = "pair", step_flops, pair_bytes
-        kname = "k_conv_lds_pair (" + " + ".join(kernels[v] for v in CONV2) + ")"
+        # the pair runs both parts in 4-wave blocks, the part with more input
+        # channels (2b) on 32 x 32 tiles, the other on 32 x 64
+        kname = "k_conv_lds_pair (conv 2a: 3x3s1 32x64 tiles + conv 2b: 3x3s2 32x32 tiles, 4-wave blocks)"
         covers, wl = "one dispatch: conv 2a and 2b paired", "conv 2a + conv 2b (one paired launch)"
     else:
         for v, c in CONV2.items():
