@@ -1368,7 +1368,7 @@ hipError_t launch_conv_lds_pair(const ConvLdsDesc& a, const ConvLdsDesc& b, int 
   ca.w = cb.w = 4;
   // a second part with more input channels (more chunks per wave) on 32 x 32
   // tiles, so its blocks carry about the first part's work and the CUs finish
-  // together (headline step 25.9 -> 24.7 us)
+  // together (headline step 26.0 -> 25.4 us)
   if (b.IC > a.IC) cb.tn = 1;
   ca.rv = use_rv(a, ca);
   cb.rv = use_rv(b, cb);
