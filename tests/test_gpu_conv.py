@@ -414,11 +414,12 @@ def test_paired_convolution_launches(gpu_ctx, orc, pkg, monkeypatch):
     float64 convolution."""
     W, I = pkg.wgx, pkg.inputs
     monkeypatch.delenv("WGX_CONV_LDS", raising=False)
-    # (pairs 1 and 2: the second part has more input channels and runs 32 x
-    # 32 tiles; pair 3: fewer, both parts on 32 x 64)
+    # (the part with more input channels runs 32 x 32 tiles: pairs 1 and 2
+    # the second part, pair 3 the first; pair 4, equal: both on 32 x 64)
     shapes = [((1, 32, 20, 24), (48, 32, 3, 3), 1, 1), ((1, 64, 16, 16), (40, 64, 3, 3), 2, 1),
               ((1, 16, 13, 10), (24, 16, 3, 3), 1, 1), ((1, 24, 21, 19), (16, 24, 3, 3), 2, 0),
-              ((1, 64, 12, 16), (32, 64, 3, 3), 1, 1), ((1, 32, 18, 20), (48, 32, 3, 3), 2, 1)]
+              ((1, 64, 12, 16), (32, 64, 3, 3), 1, 1), ((1, 32, 18, 20), (48, 32, 3, 3), 2, 1),
+              ((1, 32, 14, 18), (24, 32, 3, 3), 1, 1), ((1, 32, 16, 12), (40, 32, 3, 3), 2, 1)]
 
     def record(i, xs, ws, s, p, res=False):
         x = I.uniform(3400 + i, xs, -1, 1)
@@ -440,7 +441,7 @@ def test_paired_convolution_launches(gpu_ctx, orc, pkg, monkeypatch):
         assert gpu_ctx.last_kernel.startswith("conv_lds_f32_"), gpu_ctx.last_kernel
         return ty, want, bound, ws[1] * 9
 
-    for merge, expect in (("1", 3), ("0", 0)):
+    for merge, expect in (("1", 4), ("0", 0)):
         monkeypatch.setenv("WGX_MERGE", merge)
         gpu_ctx.reset()
         outs = [record(i, *sh, res=(i == 3)) for i, sh in enumerate(shapes)]

@@ -637,14 +637,14 @@ __global__ __launch_bounds__(512) void k_conv_lds(CParams p) {
   conv_lds_tile<DT, KH, KW, S, TM, TN, RV>(p, blockIdx.x, gridDim.x);
 }
 
-// Two independent float32 batch-1 convolutions (32 x 64 tiles, 4 waves per
-// block) in one launch: blocks [0, na) run a's tiles, the rest b's, so the
+// Two independent float32 batch-1 convolutions (32 x (32 TN) tiles, 4 waves
+// per block) in one launch: blocks [0, na) run a's tiles, the rest b's, so the
 // start-up loads of one and the reduction and stores of the other overlap
 // on the same CUs instead of following each other.
-template <int SA, bool RVA, int SB, bool RVB, int TNB>
+template <int SA, bool RVA, int SB, bool RVB, int TNA, int TNB>
 __global__ __launch_bounds__(256) void k_conv_lds_pair(CParams pa, CParams pb, int na) {
   if ((int)blockIdx.x < na)
-    conv_lds_tile<WGX_FLOAT32, 3, 3, SA, 1, 2, RVA>(pa, blockIdx.x, na);
+    conv_lds_tile<WGX_FLOAT32, 3, 3, SA, 1, TNA, RVA>(pa, blockIdx.x, na);
   else
     conv_lds_tile<WGX_FLOAT32, 3, 3, SB, 1, TNB, RVB>(pb, blockIdx.x - na, gridDim.x - na);
 }
@@ -1258,11 +1258,11 @@ bool use_rv(const ConvLdsDesc& d, const Cfg& c) {
          (d.dtype == WGX_FLOAT32 || c.cl) && !rv_off;
 }
 
-template <int SA, bool RVA, int SB, bool RVB, int TNB>
+template <int SA, bool RVA, int SB, bool RVB, int TNA, int TNB>
 hipError_t launch_pair_t(const CParams& pa, const CParams& pb, hipStream_t s) {
-  auto fn = k_conv_lds_pair<SA, RVA, SB, RVB, TNB>;
+  auto fn = k_conv_lds_pair<SA, RVA, SB, RVB, TNA, TNB>;
   const size_t w = (size_t)pa.W;  // both parts run W waves per block
-  const size_t la = w * Geo<WGX_FLOAT32, 3, 3, SA, 2, RVA>::LDS_WAVE;
+  const size_t la = w * Geo<WGX_FLOAT32, 3, 3, SA, TNA, RVA>::LDS_WAVE;
   const size_t lb = w * Geo<WGX_FLOAT32, 3, 3, SB, TNB, RVB>::LDS_WAVE;
   const size_t part = w > 1 ? w * 1 * 2 * 4 * 64 * 16 : 0;  // the waves' partial sums
   const size_t lds = std::max(std::max(la, lb), part);
@@ -1277,14 +1277,20 @@ hipError_t launch_pair_t(const CParams& pa, const CParams& pb, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int SA, bool RVA>
+// (at most one part runs 32 x 32 tiles: TNA == 1 takes TNB == 2 only)
+template <int SA, bool RVA, int TNA>
 hipError_t launch_pair_b(const CParams& pa, const CParams& pb, int sb, bool rvb, int tnb, hipStream_t s) {
-  if (tnb == 1) {
-    if (sb == 1) return rvb ? launch_pair_t<SA, RVA, 1, true, 1>(pa, pb, s) : launch_pair_t<SA, RVA, 1, false, 1>(pa, pb, s);
-    return rvb ? launch_pair_t<SA, RVA, 2, true, 1>(pa, pb, s) : launch_pair_t<SA, RVA, 2, false, 1>(pa, pb, s);
+  if constexpr (TNA == 2) {
+    if (tnb == 1) {
+      if (sb == 1)
+        return rvb ? launch_pair_t<SA, RVA, 1, true, 2, 1>(pa, pb, s) : launch_pair_t<SA, RVA, 1, false, 2, 1>(pa, pb, s);
+      return rvb ? launch_pair_t<SA, RVA, 2, true, 2, 1>(pa, pb, s) : launch_pair_t<SA, RVA, 2, false, 2, 1>(pa, pb, s);
+    }
   }
-  if (sb == 1) return rvb ? launch_pair_t<SA, RVA, 1, true, 2>(pa, pb, s) : launch_pair_t<SA, RVA, 1, false, 2>(pa, pb, s);
-  return rvb ? launch_pair_t<SA, RVA, 2, true, 2>(pa, pb, s) : launch_pair_t<SA, RVA, 2, false, 2>(pa, pb, s);
+  if (tnb != 2) return hipErrorInvalidValue;
+  if (sb == 1)
+    return rvb ? launch_pair_t<SA, RVA, 1, true, TNA, 2>(pa, pb, s) : launch_pair_t<SA, RVA, 1, false, TNA, 2>(pa, pb, s);
+  return rvb ? launch_pair_t<SA, RVA, 2, true, TNA, 2>(pa, pb, s) : launch_pair_t<SA, RVA, 2, false, TNA, 2>(pa, pb, s);
 }
 
 }  // namespace
@@ -1351,9 +1357,9 @@ hipError_t launch_conv_lds(const ConvLdsDesc& d, int cus, hipStream_t s, std::st
 }
 
 // Two independent float32 convolutions that both take the batch-1 32 x 64
-// configuration, in one launch of 4-wave blocks (k_conv_lds_pair; the second
-// part on 32 x 32 tiles when it has more input channels); the partial sums of
-// a tile are added in the order of its 4 waves.  Not
+// configuration, in one launch of 4-wave blocks (k_conv_lds_pair; the part
+// with more input channels on 32 x 32 tiles); the partial sums of a tile are
+// added in the order of its 4 waves.  Not
 // supported (hipErrorNotSupported, nothing launched) for anything else, with
 // a forced configuration (WGX_CONV_LDS) or with WGX_MERGE=0.
 hipError_t launch_conv_lds_pair(const ConvLdsDesc& a, const ConvLdsDesc& b, int cus, hipStream_t s) {
@@ -1366,20 +1372,30 @@ hipError_t launch_conv_lds_pair(const ConvLdsDesc& a, const ConvLdsDesc& b, int 
   // 4 waves per block for both (headline step, paired: 32 us at 4 waves,
   // 40 at 2, 55 at 1; 35.5 us as two launches)
   ca.w = cb.w = 4;
-  // a second part with more input channels (more chunks per wave) on 32 x 32
-  // tiles, so its blocks carry about the first part's work and the CUs finish
+  // the part with more input channels (more chunks per wave) on 32 x 32
+  // tiles, so its blocks carry about the other part's work and the CUs finish
   // together (headline step 26.0 -> 25.4 us)
-  if (b.IC > a.IC) cb.tn = 1;
+  if (b.IC > a.IC)
+    cb.tn = 1;
+  else if (a.IC > b.IC)
+    ca.tn = 1;
   ca.rv = use_rv(a, ca);
   cb.rv = use_rv(b, cb);
   const CParams pa = make_params(a, ca), pb = make_params(b, cb);
   if (pa.ntiles == 0 || pb.ntiles == 0 || (long long)pa.ntiles + pb.ntiles >= (1LL << 31)) return hipErrorNotSupported;
   if (is_dry(s)) return hipSuccess;
+  if (ca.tn == 1) {
+    if (a.sH == 1)
+      return ca.rv ? launch_pair_b<1, true, 1>(pa, pb, b.sH, cb.rv, cb.tn, s)
+                   : launch_pair_b<1, false, 1>(pa, pb, b.sH, cb.rv, cb.tn, s);
+    return ca.rv ? launch_pair_b<2, true, 1>(pa, pb, b.sH, cb.rv, cb.tn, s)
+                 : launch_pair_b<2, false, 1>(pa, pb, b.sH, cb.rv, cb.tn, s);
+  }
   if (a.sH == 1)
-    return ca.rv ? launch_pair_b<1, true>(pa, pb, b.sH, cb.rv, cb.tn, s)
-                 : launch_pair_b<1, false>(pa, pb, b.sH, cb.rv, cb.tn, s);
-  return ca.rv ? launch_pair_b<2, true>(pa, pb, b.sH, cb.rv, cb.tn, s)
-               : launch_pair_b<2, false>(pa, pb, b.sH, cb.rv, cb.tn, s);
+    return ca.rv ? launch_pair_b<1, true, 2>(pa, pb, b.sH, cb.rv, cb.tn, s)
+                 : launch_pair_b<1, false, 2>(pa, pb, b.sH, cb.rv, cb.tn, s);
+  return ca.rv ? launch_pair_b<2, true, 2>(pa, pb, b.sH, cb.rv, cb.tn, s)
+               : launch_pair_b<2, false, 2>(pa, pb, b.sH, cb.rv, cb.tn, s);
 }
 
 }  // namespace wgx
